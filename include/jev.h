@@ -1,0 +1,205 @@
+/*
+ * jev.h -- C ABI of libjev, the MI355X token loop behind Jevstral's managed API.
+ *
+ * The managed host (GgufFile, JevstralDecider, SystemPromptCache) keeps its API
+ * and calls these entry points over [LibraryImport("jev")].  Every array in a
+ * signature is a plain pointer owned by the caller and only read or written
+ * during the call.  A context owns its device weights, KV arena, scratch and
+ * HIP stream; it is not thread-safe (like MinistralModel, MinistralModel.cs:21-22):
+ * use one context per concurrent request.  Only jev_cancel may be called from
+ * another thread.
+ *
+ * Status codes map onto the reference's exceptions:
+ *   JEV_EINVAL    ArgumentException        (QuantMatMul.cs:77-80, MinistralModel.cs:306, :202-207)
+ *   JEV_EDATA     InvalidDataException     (ModelConfig.cs:108-110, MinistralModel.cs:110-123)
+ *   JEV_ECANCELED OperationCanceledException (ParallelOptions.CancellationToken)
+ *   JEV_ENOMEM / JEV_EDEVICE               HIP allocation / runtime failures
+ *   JEV_ESTATE    InvalidOperationException (call order, e.g. forward before finalize)
+ * jev_last_error() returns the thread's last message.
+ */
+#ifndef JEV_H
+#define JEV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JEV_OK 0
+#define JEV_EINVAL 1
+#define JEV_EDATA 2
+#define JEV_ENOMEM 3
+#define JEV_EDEVICE 4
+#define JEV_ECANCELED 5
+#define JEV_ESTATE 6
+
+/* GGML type ids (src/Jevstral/Gguf/GgmlType.cs:12-18). */
+#define JEV_TYPE_F32 0
+#define JEV_TYPE_F16 1
+#define JEV_TYPE_Q4_0 2
+#define JEV_TYPE_Q5_1 7
+#define JEV_TYPE_Q8_0 8
+
+/* Tensor slots: the tensors MinistralModel binds (MinistralModel.cs:74-96). */
+#define JEV_SLOT_TOKEN_EMBD 0  /* token_embd.weight                    */
+#define JEV_SLOT_OUTPUT_NORM 1 /* output_norm.weight                   */
+#define JEV_SLOT_OUTPUT 2      /* output.weight (optional; tied if absent) */
+#define JEV_SLOT_ATTN_NORM 3   /* blk.{l}.attn_norm.weight             */
+#define JEV_SLOT_Q 4           /* blk.{l}.attn_q.weight                */
+#define JEV_SLOT_K 5           /* blk.{l}.attn_k.weight                */
+#define JEV_SLOT_V 6           /* blk.{l}.attn_v.weight                */
+#define JEV_SLOT_O 7           /* blk.{l}.attn_output.weight           */
+#define JEV_SLOT_FFN_NORM 8    /* blk.{l}.ffn_norm.weight              */
+#define JEV_SLOT_GATE 9        /* blk.{l}.ffn_gate.weight              */
+#define JEV_SLOT_UP 10         /* blk.{l}.ffn_up.weight                */
+#define JEV_SLOT_DOWN 11       /* blk.{l}.ffn_down.weight              */
+
+/* Output modes of the private ForwardAsync (MinistralModel.cs:301-425). */
+#define JEV_OUT_NONE 0      /* PrefillAsync: KV state only (:148-149)                       */
+#define JEV_OUT_LAST_FULL 1 /* computeLogits: full vocabulary at the last token (:411-424)  */
+#define JEV_OUT_SELECTED 2  /* selectedRows at every output token (:386-410)               */
+#define JEV_OUT_FULL 3      /* full vocabulary at every output token (:362-385)            */
+
+/* ModelConfig (ModelConfig.cs:12-118): filled by the managed side from the GGUF
+ * metadata it already parses (ModelConfig.FromGguf). */
+typedef struct jev_config {
+    int32_t n_layers;       /* {arch}.block_count                          */
+    int32_t hidden;         /* {arch}.embedding_length                     */
+    int32_t n_heads;        /* {arch}.attention.head_count                 */
+    int32_t n_kv_heads;     /* {arch}.attention.head_count_kv              */
+    int32_t head_dim;       /* {arch}.attention.key_length (must be 128)   */
+    int32_t ffn;            /* {arch}.feed_forward_length                  */
+    int32_t vocab;          /* tokenizer.ggml.tokens length                */
+    float rms_eps;          /* {arch}.attention.layer_norm_rms_epsilon     */
+    float rope_freq_base;   /* {arch}.rope.freq_base                       */
+    int32_t rope_dim;       /* {arch}.rope.dimension_count                 */
+    float rope_scale_factor;/* {arch}.rope.scaling.factor                  */
+    int32_t rope_scaling_yarn; /* {arch}.rope.scaling.type == "yarn"       */
+    int32_t rope_original_context;
+    float yarn_beta_fast, yarn_beta_slow, yarn_ext_factor, yarn_mscale, yarn_mscale_all_dim;
+    float rope_attn_factor;
+    float attention_temperature_scale;
+    int32_t initial_kv_capacity; /* MinistralModel(path, initialCacheCapacity) */
+} jev_config;
+
+/* TokenLayout (MinistralModel.cs:703-781): token t is written to cache slot
+ * slot[t], rotated as position[t], and attends to slots [shared_lo[t],
+ * shared_hi[t]) and to its own segment [segment[t], slot[t]].  The reference's
+ * layouts are shared_lo = 0 and shared_hi = Shared; a nonzero shared_lo lets
+ * independent decisions keep their own trunks in one cache.  outputs lists the
+ * tokens whose logits are returned; end is one past the highest slot written. */
+typedef struct jev_layout {
+    const int32_t *slot;
+    const int32_t *position;
+    const int32_t *shared_lo;
+    const int32_t *shared_hi;
+    const int32_t *segment;
+    const int32_t *outputs;
+    int32_t n_outputs;
+    int32_t end;
+} jev_layout;
+
+typedef struct jev_ctx jev_ctx;
+
+const char *jev_last_error(void);
+
+/* new MinistralModel(...) minus the GGUF parse: validates the config and
+ * allocates the KV arena (KvCache ctor, KvCache.cs:25-33) on `device`. */
+int jev_create(const jev_config *cfg, int device, jev_ctx **out);
+void jev_destroy(jev_ctx *ctx);
+
+/* WeightMatrix.From / VectorParameter.From (WeightMatrix.cs:53-90): copies one
+ * GGUF tensor (rows = Shape[1], cols = Shape[0]; bytes = GgufFile.GetTensorPointer)
+ * into HBM, repacked for the kernels.  `layer` is ignored for global slots. */
+int jev_bind_tensor(jev_ctx *ctx, int slot, int layer, int ggml_type, int64_t rows, int64_t cols,
+                    const void *bytes, size_t nbytes);
+/* MinistralModel.ValidateShapes (MinistralModel.cs:110-123) plus the
+ * every-tensor-present check of its constructor. */
+int jev_finalize(jev_ctx *ctx);
+
+/* KvCache (KvCache.cs). */
+int jev_kv_length(jev_ctx *ctx, int32_t *length);
+int jev_kv_capacity(jev_ctx *ctx, int32_t *capacity);
+int jev_kv_reserve(jev_ctx *ctx, int32_t required);              /* EnsureCapacity :48-70 */
+int jev_kv_truncate(jev_ctx *ctx, int32_t length);               /* Truncate :46          */
+int jev_kv_reset(jev_ctx *ctx);                                  /* Reset :43             */
+int jev_kv_snapshot(jev_ctx *ctx, int32_t length, float *out, size_t n_floats); /* Snapshot :94-112 */
+int jev_kv_restore(jev_ctx *ctx, const float *in, size_t n_floats, int32_t length); /* Restore :115-136 */
+
+/* The private ForwardAsync (MinistralModel.cs:301-435).  layout NULL = plain
+ * causal append after the cached tokens.  out receives (by mode): nothing;
+ * vocab floats; n_outputs * n_rows floats; n_outputs * vocab floats, where
+ * n_outputs is 1 without a layout. */
+int jev_forward(jev_ctx *ctx, const int32_t *tokens, int32_t n_tokens, const jev_layout *layout, int mode,
+                const int32_t *rows, int32_t n_rows, float *out, size_t out_len);
+
+/* ForwardTreeAsync (MinistralModel.cs:198-219): the trunk appended causally,
+ * then every branch continuing from its end; branch_tokens holds the branches
+ * back to back.  out = n_branches * n_rows verdict-row logits. */
+int jev_forward_tree(jev_ctx *ctx, const int32_t *trunk, int32_t n_trunk, const int32_t *branch_tokens,
+                     const int32_t *branch_lens, int32_t n_branches, const int32_t *rows, int32_t n_rows,
+                     float *out, size_t out_len);
+
+/* Greedy decode (Benchmark.cs:411-422 / ReasoningDecider.cs:157-178): feeds
+ * `first`, then n_steps - 1 argmax tokens, one ForwardAsync([next]) each;
+ * tokens_out receives the n_steps argmax ids (Kernels.ArgMax, lowest index on ties). */
+int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tokens_out);
+
+/* JevstralDecider.DecideAsync margins (:306-308) and softmax(z/T) (:310-313):
+ * verdicts is n_options x (n_yes + n_no). */
+int jev_margins(const float *verdicts, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature,
+                float *margins, float *probs);
+
+/* ParallelOptions.CancellationToken: polled between layers; the forward in
+ * flight returns JEV_ECANCELED and the flag clears. */
+void jev_cancel(jev_ctx *ctx);
+
+/* Timing support: device-resident variant of jev_forward for a fixed plan.
+ * d_tokens / d_out are device pointers; the call only enqueues work on the
+ * context's stream (no host synchronisation); jev_sync waits for it. */
+int jev_forward_device(jev_ctx *ctx, const int32_t *d_tokens, int32_t n_tokens, const jev_layout *layout, int mode,
+                       const int32_t *rows, int32_t n_rows, float *d_out);
+int jev_sync(jev_ctx *ctx);
+/* The context's HIP stream (hipStream_t), for event timing by the caller. */
+void *jev_stream(jev_ctx *ctx);
+
+/* Kernel timing: with profiling enabled, the context records a HIP event pair
+ * around every launch of the listed kernel classes on its own stream, and
+ * accumulates launches, device time and algorithmic work (FLOPs of the
+ * product, bytes of the weights and activations it must move).  Enabling
+ * clears the counters; reading synchronises the stream. */
+#define JEV_PROF_GEMM 0 /* MFMA prefill GEMM                     */
+#define JEV_PROF_ATTN 1 /* tree attention (prefill)              */
+#define JEV_PROF_GEMV 2 /* one-token quantized GEMV              */
+#define JEV_PROF_DECODE_ATTN 3 /* decode attention + combine     */
+#define JEV_PROF_CLASSES 4
+int jev_profile_enable(jev_ctx *ctx, int enable);
+int jev_profile_read(jev_ctx *ctx, int kernel_class, int64_t *launches, double *total_ms, double *flops,
+                     double *bytes);
+
+/* ---- Test hooks (no managed counterpart) ---- */
+
+/* Dequantizer.Dequantize (Dequantizer.cs:45-93) run on the device:
+ * `count` elements from GGUF blocks to float32. */
+int jev_dequantize(int ggml_type, const void *src, size_t nbytes, float *dst, int64_t count);
+/* QuantMatMul.ForwardAsync (QuantMatMul.cs:66-121) run on the device: tokens >= 2
+ * take the MFMA GEMM, 1 token the GEMV.  y = tokens x rows. */
+int jev_matmul_q(int ggml_type, const void *w, int64_t rows, int64_t cols, const float *x, int32_t tokens, float *y);
+
+/* ---- Synthetic-model tool (replaces the converter for offline runs) ---- */
+
+/* ggml reference quantizers (quantize_row_q8_0/q4_0/q5_1_ref) over `count`
+ * floats into GGUF blocks. */
+int jev_quantize(int ggml_type, const float *src, int64_t count, void *dst, size_t nbytes);
+/* Fills a rows x cols tensor with N(0, stddev) draws from a counter-based
+ * generator keyed by (seed, stream), quantized to ggml_type (F32 writes floats).
+ * The bytes depend only on (seed, stream, shape, type), not on `threads`. */
+int jev_synth_tensor(uint64_t seed, uint64_t stream, int ggml_type, int64_t rows, int64_t cols, float stddev,
+                     void *dst, size_t nbytes, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,188 @@
+// Internal interfaces of libjev: device weight layout, kernel launchers and
+// the host-side quantizer / repack helpers.  Not part of the C ABI.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+namespace jev {
+
+// GGML type ids (GgmlType.cs:12-18).
+enum : int { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ5_1 = 7, kQ8_0 = 8 };
+
+int block_size(int type);           // elements per block (GgmlType.cs:55-64)
+int type_size(int type);            // bytes per block    (GgmlType.cs:67-82)
+int64_t row_bytes(int type, int64_t cols);
+
+// ---------------------------------------------------------------- layout
+//
+// A quantized 2-D weight in HBM, split by field so every kernel load is an
+// aligned vector load (a GGUF block is 34, 24 or 18 bytes, which no 16-byte
+// load can follow):
+//   Q8_0: qs  int8  [rows][cols]        the 32 quants of each block in order
+//         d   fp16  [rows][cols/32]
+//   Q4_0: qs  uint8 [rows][cols/2]      each block's 16 bytes unchanged (byte j =
+//         d   fp16  [rows][cols/32]      element j low nibble, j+16 high nibble)
+//   Q5_1: qs  uint8 [rows][cols/2]      as Q4_0
+//         qh  uint32[rows][cols/32]     the block's fifth bits, unchanged
+//         d,m fp16  [rows][cols/32]
+struct QWeight {
+    int type = -1;
+    int rows = 0, cols = 0;
+    const uint8_t *qs = nullptr;
+    const uint16_t *d = nullptr;
+    const uint16_t *m = nullptr;
+    const uint32_t *qh = nullptr;
+    void *base = nullptr; // owning allocation
+    size_t bytes = 0;
+};
+
+// Byte offsets of the fields inside one allocation of the layout above.
+struct QLayout {
+    size_t qs, d, m, qh, total;
+};
+QLayout qlayout(int type, int64_t rows, int64_t cols);
+
+// Host: GGUF blocks (rows x cols) -> the field-split layout in `dst`
+// (qlayout(type, rows, cols).total bytes).  Returns false on a bad type/shape.
+bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *dst, int threads);
+
+// Host scalar helpers.
+float half_to_float(uint16_t h);
+uint16_t float_to_half(float f); // round to nearest even
+
+// ---------------------------------------------------------------- kernels
+
+// Dequantize `rows` full rows of a weight into fp32 [rows][cols].
+hipError_t launch_dequant(const QWeight &w, float *dst, hipStream_t s);
+
+// Embedding gather: h[t] = decode(row ids[t]).
+hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, hipStream_t s);
+
+// GEMM y = x . W^T with x given as an fp16 hi/lo pair (x ~= hi + lo) and W
+// quantized.  Every output is computed in an order that does not depend on M.
+enum GemmMode : int {
+    kGemmStore = 0,  // y fp32 [M][ldy]   (ldy = total columns of all segments)
+    kGemmSwiGlu = 1, // seg 0 = gate, seg 1 = up: out = silu(g)*u as fp16 hi/lo [M][N_gate]
+};
+struct GemmArgs {
+    int M = 0, K = 0;
+    const uint16_t *xhi = nullptr, *xlo = nullptr; // fp16 bits [M][K]
+    const float *xsum = nullptr;                   // Q5_1 only: per-32 block sums [M][K/32]
+    int nseg = 1;
+    QWeight seg[3];
+    int ldy = 0;
+    float *y = nullptr;
+    int ksplit = 1;                      // fixed per (N, K); partials at y + z*M*ldy
+    uint16_t *ohi = nullptr, *olo = nullptr; // SwiGLU output, ld = seg[0].rows
+    int mode = kGemmStore;
+};
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+// y[m][n] = sum_z partial[z][m][n] (+ res[m][n] if res), z ascending.
+hipError_t launch_reduce_partials(const float *partial, int ksplit, int M, int N, float *y, hipStream_t s);
+
+// GEMV for one token: y[r] = dot(x, W[r]) with fp32 x.  Up to 3 segments
+// (outputs concatenated), or a gate/up pair with SwiGLU fused (y = silu(g)*u).
+struct GemvArgs {
+    int K = 0;
+    const float *x = nullptr;
+    int nseg = 1;
+    QWeight seg[3];
+    float *y = nullptr;
+    int swiglu = 0;
+};
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
+
+// Row kernels.
+//  rmsnorm: if add != nullptr, h[t] += add[t] first (stored back).  Output is
+//  either fp32 (out32) or an fp16 hi/lo pair; xsum (optional) receives per-32
+//  block sums of the normalised row.
+struct NormArgs {
+    int T = 0, D = 0;
+    float *h = nullptr;
+    const float *add = nullptr;
+    bool store_h = true;           // write h + add back into h
+    const float *w = nullptr;
+    float eps = 1e-5f;
+    const int32_t *rows = nullptr; // optional row indices into h (output rows)
+    float *out32 = nullptr;
+    uint16_t *ohi = nullptr, *olo = nullptr;
+    float *xsum = nullptr;
+};
+hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s);
+
+// x -> (hi, lo) fp16 pair.
+hipError_t launch_split(const float *x, size_t n, uint16_t *hi, uint16_t *lo, hipStream_t s);
+
+// Per-32 block sums of an fp16 hi/lo activation (Q5_1 offset term).
+hipError_t launch_block_sums(const uint16_t *hi, const uint16_t *lo, int T, int D, float *xsum, hipStream_t s);
+
+// RoPE + KV store: y is [T][qdim + 2*kvdim] (q | k | v) or separate pointers.
+struct RopeArgs {
+    int T = 0, n_heads = 0, n_kv = 0, hd = 128, half = 64;
+    const float *q_in = nullptr, *k_in = nullptr, *v_in = nullptr;
+    int ld_in = 0;
+    float *q_out = nullptr; // [T][qdim]
+    float *kc = nullptr, *vc = nullptr; // layer base: [kvh][cap][hd]
+    int cap = 0;
+    const int32_t *pos = nullptr, *slot = nullptr;
+    int start = 0; // used when pos/slot are null (causal append)
+    const float *freqs = nullptr;
+    float mscale = 1.f;
+    int orig_ctx = 0;
+    float temp_scale = 0.f;
+};
+hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s);
+
+// Tree-masked attention tiles: consecutive tokens sharing (shared_lo,
+// shared_hi, segment) with consecutive slots, at most 64 per tile.
+struct AttnTile {
+    int32_t t0, n, shared_lo, shared_hi, segment, slot0, pad0, pad1;
+};
+struct AttnArgs {
+    int n_tiles = 0, n_heads = 0, group = 4, hd = 128;
+    const AttnTile *tiles = nullptr;
+    const float *q = nullptr; // [T][qdim]
+    const float *kc = nullptr, *vc = nullptr; // layer base [kvh][cap][hd]
+    int cap = 0;
+    float scale = 0.f;
+    uint16_t *ohi = nullptr, *olo = nullptr; // [T][qdim]
+};
+hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
+
+// Decode attention: one query token per entry, split over 64-key chunks,
+// partials combined in chunk order.  ctx fp32 [T][qdim].
+struct DecodeAttnArgs {
+    int T = 0, n_heads = 0, group = 4, hd = 128, max_chunks = 0;
+    const float *q = nullptr;
+    const float *kc = nullptr, *vc = nullptr;
+    int cap = 0;
+    const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
+    int start = 0; // causal append when the arrays are null
+    float scale = 0.f;
+    float *part = nullptr; // [T][heads][max_chunks][hd + 2]
+    float *ctx = nullptr;
+};
+hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
+
+// Verdict-row head: for each output b, logits[b][i] = dot(norm(h[outputs[b]]), W[rows[i]]).
+struct HeadRowsArgs {
+    int n_out = 0, n_rows = 0, D = 0;
+    const float *xn = nullptr; // normalised output rows [n_out][D]
+    QWeight table;
+    const int32_t *rows = nullptr;
+    float *out = nullptr;
+};
+hipError_t launch_head_rows(const HeadRowsArgs &a, hipStream_t s);
+
+// Lowest index of the maximum of x[0..n).
+hipError_t launch_argmax(const float *x, int n, int32_t *result, float *scratch_val, int32_t *scratch_idx,
+                         hipStream_t s);
+
+// KV copy for capacity growth: [L*kvh] heads of `len` rows from stride old_cap to new_cap.
+hipError_t launch_kv_copy(const float *src, float *dst, int heads_total, int old_cap, int new_cap, int len, int hd,
+                          hipStream_t s);
+
+} // namespace jev

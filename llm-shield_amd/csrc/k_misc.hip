@@ -1,0 +1,338 @@
+// Row-wise and small kernels of the token loop: dequantize, embedding gather,
+// fused residual-add + RMSNorm, RoPE + KV store, verdict-row head, argmax,
+// split-K reduction and KV-arena growth.  All HBM-bound; every reduction has
+// a fixed order so results are reproducible bit for bit.
+#include "jev_dev.h"
+
+namespace jev {
+
+// ------------------------------------------------------------ dequant / gather
+
+__global__ void dequant_kernel(QWeight w, float *dst)
+{
+    int r = blockIdx.x;
+    for (int k = threadIdx.x; k < w.cols; k += blockDim.x) dst[(size_t)r * w.cols + k] = decode_elem(w, r, k);
+}
+
+hipError_t launch_dequant(const QWeight &w, float *dst, hipStream_t s)
+{
+    if (w.rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(dequant_kernel, dim3(w.rows), dim3(256), 0, s, w, dst);
+    return hipGetLastError();
+}
+
+// QuantMatMul.GatherRows (QuantMatMul.cs:294-305): ids are validated on the host.
+__global__ void gather_kernel(QWeight w, const int32_t *ids, float *h)
+{
+    int t = blockIdx.x;
+    int r = ids[t];
+    for (int k = threadIdx.x; k < w.cols; k += blockDim.x) h[(size_t)t * w.cols + k] = decode_elem(w, r, k);
+}
+
+hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_kernel, dim3(n), dim3(256), 0, s, w, ids, h);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ RMSNorm
+
+// Kernels.RmsNorm (Kernels.cs:25-60) as one workgroup per row: each thread
+// sums the squares of its strided elements in fp32, waves reduce by a fixed
+// butterfly, the four wave sums combine in double; then
+// scale = 1 / sqrt((float)(sum / n) + eps) and y = (x * scale) * w.
+// With `add`, the residual step h += add (Kernels.Add) comes first.
+constexpr int kNormSumMax = 8192;
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
+{
+    __shared__ double wsum[4];
+    int t = blockIdx.x;
+    int row = a.rows ? a.rows[t] : t;
+    float *h = a.h + (size_t)row * a.D;
+    const float *add = a.add ? a.add + (size_t)row * a.D : nullptr;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < a.D; i += 256) {
+        float v = h[i];
+        if (add) {
+            v = v + add[i];
+            if (a.store_h) h[i] = v;
+        }
+        float sq = v * v;
+        ss = ss + sq;
+    }
+    ss = warp_sum(ss);
+    int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) wsum[wv] = (double)ss;
+    __syncthreads();
+    double sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    float scale = 1.0f / sqrtf((float)(sum / a.D) + a.eps);
+    for (int i = threadIdx.x; i < a.D; i += 256) {
+        float x = add && !a.store_h ? h[i] + add[i] : h[i];
+        float v = x * scale;
+        float y = v * a.w[i];
+        size_t o = (size_t)t * a.D + i;
+        if (a.out32) a.out32[o] = y;
+        if (a.ohi) {
+            uint16_t hi, lo;
+            split_f16(y, hi, lo);
+            a.ohi[o] = hi;
+            a.olo[o] = lo;
+        }
+    }
+    if (a.xsum) {
+        // Per-32 block sums of the (hi + lo) values the GEMM will see, staged
+        // through LDS (the host only asks for them when D <= kNormSumMax).
+        __shared__ float stage[kNormSumMax];
+        for (int i = threadIdx.x; i < a.D; i += 256) {
+            size_t o = (size_t)t * a.D + i;
+            stage[i] = h2f(a.ohi[o]) + h2f(a.olo[o]);
+        }
+        __syncthreads();
+        int nb = a.D >> 5;
+        for (int b = threadIdx.x; b < nb; b += 256) {
+            float s = 0.f;
+            for (int j = 0; j < 32; j++) s += stage[b * 32 + j];
+            a.xsum[(size_t)t * nb + b] = s;
+        }
+    }
+}
+
+hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
+{
+    if (a.T <= 0) return hipSuccess;
+    if (a.xsum && (a.D > kNormSumMax || !a.ohi)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+__global__ void block_sums_kernel(const uint16_t *hi, const uint16_t *lo, int D, float *xsum)
+{
+    int t = blockIdx.x;
+    int nb = D >> 5;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+        float s = 0.f;
+        for (int j = 0; j < 32; j++) {
+            size_t o = (size_t)t * D + b * 32 + j;
+            s += h2f(hi[o]) + h2f(lo[o]);
+        }
+        xsum[(size_t)t * nb + b] = s;
+    }
+}
+
+hipError_t launch_block_sums(const uint16_t *hi, const uint16_t *lo, int T, int D, float *xsum, hipStream_t s)
+{
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(block_sums_kernel, dim3(T), dim3(128), 0, s, hi, lo, D, xsum);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ RoPE + KV store
+
+// Rope.Apply (Rope.cs:112-135) for q and k of one token, then
+// ApplyPositionScale on q (MinistralModel.cs:676-682); k and v land in their
+// cache slots (StoreKeys / StoreValues, :649-669).  cos/sin are computed in
+// float from position * freq with the accurate library functions.
+__global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
+{
+    __shared__ float cs[512], sn[512];
+    int t = blockIdx.x;
+    int pos = a.pos ? a.pos[t] : a.start + t;
+    int slot = a.slot ? a.slot[t] : a.start + t;
+    for (int i = threadIdx.x; i < a.half; i += 256) {
+        float theta = (float)pos * a.freqs[i];
+        cs[i] = cosf(theta) * a.mscale;
+        sn[i] = sinf(theta) * a.mscale;
+    }
+    __syncthreads();
+    float qscale = 1.f;
+    bool scaled = false;
+    if (a.orig_ctx > 0 && a.temp_scale != 0.f) {
+        float interval = floorf((float)pos / (float)a.orig_ctx);
+        if (interval != 0.f) {
+            qscale = 1.f + a.temp_scale * logf(1.f + interval);
+            scaled = true;
+        }
+    }
+    int qdim = a.n_heads * a.hd, kvdim = a.n_kv * a.hd;
+    const float *qi = a.q_in + (size_t)t * a.ld_in;
+    const float *ki = a.k_in + (size_t)t * a.ld_in;
+    const float *vi = a.v_in + (size_t)t * a.ld_in;
+    float *qo = a.q_out + (size_t)t * qdim;
+    int hpairs = a.hd >> 1;
+    for (int p = threadIdx.x; p < (qdim >> 1); p += 256) {
+        int i = p % hpairs;
+        float x0 = qi[2 * p], x1 = qi[2 * p + 1];
+        float o0 = x0, o1 = x1;
+        if (i < a.half) {
+            float c = cs[i], sv = sn[i];
+            float m0 = x0 * c, m1 = x1 * sv, m2 = x0 * sv, m3 = x1 * c;
+            o0 = m0 - m1;
+            o1 = m2 + m3;
+        }
+        if (scaled) {
+            o0 = o0 * qscale;
+            o1 = o1 * qscale;
+        }
+        qo[2 * p] = o0;
+        qo[2 * p + 1] = o1;
+    }
+    for (int p = threadIdx.x; p < (kvdim >> 1); p += 256) {
+        int i = p % hpairs;
+        int h = (2 * p) / a.hd, d = (2 * p) % a.hd;
+        float x0 = ki[2 * p], x1 = ki[2 * p + 1];
+        float o0 = x0, o1 = x1;
+        if (i < a.half) {
+            float c = cs[i], sv = sn[i];
+            float m0 = x0 * c, m1 = x1 * sv, m2 = x0 * sv, m3 = x1 * c;
+            o0 = m0 - m1;
+            o1 = m2 + m3;
+        }
+        float *kd = a.kc + ((size_t)h * a.cap + slot) * a.hd + d;
+        kd[0] = o0;
+        kd[1] = o1;
+        float *vd = a.vc + ((size_t)h * a.cap + slot) * a.hd + d;
+        vd[0] = vi[2 * p];
+        vd[1] = vi[2 * p + 1];
+    }
+}
+
+hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
+{
+    if (a.T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_store_kernel, dim3(a.T), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ verdict-row head
+
+// One wave per (output, selected row): the decoded row dotted with the
+// normalised output state (MinistralModel.cs:386-410), lane-strided fp32 FMA
+// chains reduced by a fixed butterfly.
+__global__ __launch_bounds__(64) void head_rows_kernel(HeadRowsArgs a)
+{
+    int b = blockIdx.x, i = blockIdx.y;
+    int r = a.rows[i];
+    const float *x = a.xn + (size_t)b * a.D;
+    float acc = 0.f;
+    for (int k = threadIdx.x; k < a.D; k += 64) acc = fmaf(x[k], decode_elem(a.table, r, k), acc);
+    acc = warp_sum(acc);
+    if (threadIdx.x == 0) a.out[(size_t)b * a.n_rows + i] = acc;
+}
+
+hipError_t launch_head_rows(const HeadRowsArgs &a, hipStream_t s)
+{
+    if (a.n_out <= 0 || a.n_rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(head_rows_kernel, dim3(a.n_out, a.n_rows), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ argmax
+
+// Kernels.ArgMax (Kernels.cs:146): index of the largest element, lowest index
+// on ties.  Pass 1: one (value, index) per block; pass 2: one block over those.
+__device__ __forceinline__ void better(float &v, int &i, float v2, int i2)
+{
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, float *ov, int32_t *oi)
+{
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int k = blockIdx.x * 256 + threadIdx.x; k < n; k += gridDim.x * 256) better(v, idx, x[k], k);
+    sv[threadIdx.x] = v;
+    si[threadIdx.x] = idx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            float v2 = sv[threadIdx.x + o];
+            int i2 = si[threadIdx.x + o];
+            float v1 = sv[threadIdx.x];
+            int i1 = si[threadIdx.x];
+            better(v1, i1, v2, i2);
+            sv[threadIdx.x] = v1;
+            si[threadIdx.x] = i1;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        ov[blockIdx.x] = sv[0];
+        oi[blockIdx.x] = si[0];
+    }
+}
+
+hipError_t launch_argmax(const float *x, int n, int32_t *result, float *sv, int32_t *si, hipStream_t s)
+{
+    const int blocks = 256;
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, x, n, sv, si);
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, s, (const float *)sv, blocks, sv + blocks, si + blocks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return hipMemcpyAsync(result, si + blocks, sizeof(int32_t), hipMemcpyDeviceToDevice, s);
+}
+
+// ------------------------------------------------------------ fp32 -> fp16 pair
+
+__global__ void split_kernel(const float *x, size_t n, uint16_t *hi, uint16_t *lo)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint16_t a, b;
+    split_f16(x[i], a, b);
+    hi[i] = a;
+    lo[i] = b;
+}
+
+hipError_t launch_split(const float *x, size_t n, uint16_t *hi, uint16_t *lo, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, hi, lo);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ split-K reduce
+
+__global__ void reduce_partials_kernel(const float *p, int ksplit, size_t mn, float *y)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= mn) return;
+    float s = p[i];
+    for (int z = 1; z < ksplit; z++) s = s + p[(size_t)z * mn + i];
+    y[i] = s;
+}
+
+hipError_t launch_reduce_partials(const float *partial, int ksplit, int M, int N, float *y, hipStream_t s)
+{
+    size_t mn = (size_t)M * N;
+    if (mn == 0) return hipSuccess;
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, partial, ksplit, mn, y);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ KV growth
+
+__global__ void kv_copy_kernel(const float *src, float *dst, int old_cap, int new_cap, int len, int hd)
+{
+    int h = blockIdx.y;
+    size_t n = (size_t)len * hd;
+    const float *s = src + (size_t)h * old_cap * hd;
+    float *d = dst + (size_t)h * new_cap * hd;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) d[i] = s[i];
+}
+
+hipError_t launch_kv_copy(const float *src, float *dst, int heads_total, int old_cap, int new_cap, int len, int hd,
+                          hipStream_t s)
+{
+    if (len <= 0 || heads_total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_copy_kernel, dim3(64, heads_total), dim3(256), 0, s, src, dst, old_cap, new_cap, len, hd);
+    return hipGetLastError();
+}
+
+} // namespace jev

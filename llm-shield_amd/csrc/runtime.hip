@@ -1,0 +1,1302 @@
+// libjev host runtime: the C ABI of include/jev.h.
+//
+// Mirrors MinistralModel (MinistralModel.cs) behind the managed API: weights are
+// bound once into HBM, the KV cache is a device arena laid out like KvCache
+// ([layer][kv head][capacity][128] fp32, KvCache.cs:18-19, :75), and the
+// private ForwardAsync (:301-435) becomes one enqueue of HIP kernels on the
+// context's stream.  Calls of two or more tokens take the MFMA path (GEMM +
+// tree attention), one-token calls the GEMV path (decode), as the reference
+// switches between PanelGemm and the row-wise float dot at PanelMinTokens = 2
+// (QuantMatMul.cs:51, :84).
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/jev.h"
+#include "jev_internal.h"
+
+using namespace jev;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                                          \
+    do {                                                                                                       \
+        hipError_t e_ = (expr);                                                                                \
+        if (e_ != hipSuccess) return fail(JEV_EDEVICE, "%s failed: %s", #expr, hipGetErrorString(e_));         \
+    } while (0)
+
+int host_threads()
+{
+    unsigned n = std::thread::hardware_concurrency();
+    return n == 0 ? 4 : (int)std::min(16u, n);
+}
+
+// A device buffer that only grows.
+template <typename T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t n = 0;
+    hipError_t ensure(size_t need)
+    {
+        if (need <= n) return hipSuccess;
+        if (p) {
+            // work queued on any stream may still read the old buffer
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return e;
+            e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            n = 0;
+        }
+        hipError_t e = hipMalloc((void **)&p, std::max<size_t>(need, 1) * sizeof(T));
+        if (e == hipSuccess) n = need;
+        return e;
+    }
+    void release()
+    {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+struct Layer {
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+    QWeight q, k, v, o, gate, up, down;
+};
+
+bool is_quant(int type) { return type == kQ8_0 || type == kQ4_0 || type == kQ5_1; }
+
+void free_weight(QWeight &w)
+{
+    if (w.base) (void)hipFree(w.base);
+    w = QWeight();
+}
+
+} // namespace
+
+struct jev_ctx {
+    jev_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    QWeight embd, output;
+    float *out_norm = nullptr;
+    std::vector<Layer> layers;
+    float *freqs = nullptr;
+    int half = 0;
+    float mscale = 1.f;
+    bool finalized = false;
+    std::atomic<int> cancel{0};
+
+    // KV arena
+    float *kc = nullptr, *vc = nullptr;
+    int cap = 0, len = 0;
+
+    // workspace
+    DevBuf<float> h, y, yo, ydown, q, x32, ctx32, f32, xn, logits, part, xsum;
+    DevBuf<uint16_t> xhi, xlo, fhi, flo;
+    DevBuf<int32_t> ints;
+    DevBuf<AttnTile> tiles;
+    DevBuf<float> amax_v;
+    DevBuf<int32_t> amax_i;
+    std::vector<int32_t> host_ints;
+    std::vector<AttnTile> host_tiles;
+    // Pinned staging for the per-call metadata upload; `copied` marks when the
+    // previous upload has left it.
+    int32_t *pin_ints = nullptr;
+    size_t pin_ints_n = 0;
+    AttnTile *pin_tiles = nullptr;
+    size_t pin_tiles_n = 0;
+    hipEvent_t copied = nullptr;
+
+    // Kernel timing (jev_profile_enable).
+    struct ProfRec {
+        int cls;
+        hipEvent_t a, b;
+        double flops, bytes;
+    };
+    bool profiling = false;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_used = 0;
+    std::vector<ProfRec> prof;
+
+    int qdim() const { return cfg.n_heads * cfg.head_dim; }
+    int kvdim() const { return cfg.n_kv_heads * cfg.head_dim; }
+    const QWeight &table() const { return output.base ? output : embd; }
+    size_t layer_stride() const { return (size_t)cfg.n_kv_heads * cap * cfg.head_dim; }
+};
+
+// ---------------------------------------------------------------- helpers
+
+namespace {
+
+// Rope ctor (Rope.cs:33-66) on the host: the frequency table both the
+// prefill and the decode path rotate with.
+int rope_table(const jev_config &c, std::vector<float> &freqs, float &mscale)
+{
+    int half = c.rope_dim / 2;
+    freqs.assign(half, 0.f);
+    float freq_scale = 1.0f / c.rope_scale_factor;
+    bool yarn = c.rope_scaling_yarn && c.rope_original_context > 0 && c.yarn_ext_factor != 0.0f &&
+                c.rope_scale_factor > 1.0f; // ModelConfig.YarnActive (ModelConfig.cs:54-56)
+    if (!yarn) {
+        for (int i = 0; i < half; i++)
+            freqs[i] = freq_scale / powf(c.rope_freq_base, 2.0f * (float)i / (float)c.rope_dim);
+        mscale = c.rope_attn_factor;
+        return half;
+    }
+    float low, high;
+    if (c.yarn_beta_fast == 0.0f && c.yarn_beta_slow == 0.0f) { // YarnCorrectionDims (Rope.cs:91-106)
+        low = 3.402823466e+38f;
+        high = (float)c.rope_dim / 2.0f - 1.0f;
+    } else {
+        const float pi = 3.14159265358979323846f;
+        float dims = (float)c.rope_dim, base = c.rope_freq_base;
+        auto corr = [&](float rot) { return dims * logf((float)c.rope_original_context / (rot * 2.0f * pi)) / (2.0f * logf(base)); };
+        low = fmaxf(0.0f, floorf(corr(c.yarn_beta_fast)));
+        high = fminf(dims / 2.0f - 1.0f, ceilf(corr(c.yarn_beta_slow)));
+    }
+    for (int i = 0; i < half; i++) {
+        float extrapolated = 1.0f / powf(c.rope_freq_base, 2.0f * (float)i / (float)c.rope_dim);
+        float interpolated = freq_scale * extrapolated;
+        float yv = ((float)i - low) / fmaxf(0.001f, high - low);
+        float cl = std::min(1.0f, std::max(0.0f, yv));
+        float mix = (1.0f - cl) * c.yarn_ext_factor;
+        float a = interpolated * (1.0f - mix);
+        float b = extrapolated * mix;
+        freqs[i] = a + b;
+    }
+    auto ms = [](float scale, float m) { return scale <= 1.0f ? 1.0f : 0.1f * m * logf(scale) + 1.0f; };
+    float factor = c.rope_scale_factor; // ComputeMagnitudeScale (Rope.cs:78-88)
+    float m = c.yarn_mscale != 0.0f ? c.yarn_mscale : 1.0f;
+    float ratio = c.yarn_mscale_all_dim != 0.0f ? ms(factor, m) / ms(factor, c.yarn_mscale_all_dim) : ms(factor, 1.0f);
+    mscale = ratio * c.rope_attn_factor;
+    return half;
+}
+
+// Event pair around one launch when profiling (no-op otherwise).
+struct ProfScope {
+    jev_ctx *c;
+    int cls;
+    double flops, bytes;
+    hipEvent_t a = nullptr;
+    ProfScope(jev_ctx *ctx, int k, double f, double b) : c(ctx), cls(k), flops(f), bytes(b)
+    {
+        if (!c->profiling) return;
+        a = next_event();
+        (void)hipEventRecord(a, c->stream);
+    }
+    ~ProfScope()
+    {
+        if (!a) return;
+        hipEvent_t b2 = next_event();
+        (void)hipEventRecord(b2, c->stream);
+        c->prof.push_back({cls, a, b2, flops, bytes});
+    }
+    hipEvent_t next_event()
+    {
+        if (c->ev_used == c->ev_pool.size()) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            c->ev_pool.push_back(e);
+        }
+        return c->ev_pool[c->ev_used++];
+    }
+};
+
+double weight_bytes(const QWeight &w) { return (double)row_bytes(w.type, w.cols) * w.rows; }
+
+// Uploads GGUF rows into a field-split HBM weight.
+int upload_weight(int type, int64_t rows, int64_t cols, const void *bytes, QWeight &w)
+{
+    QLayout L = qlayout(type, rows, cols);
+    std::vector<uint8_t> staging(L.total);
+    if (!repack_host(type, rows, cols, bytes, staging.data(), host_threads()))
+        return fail(JEV_EINVAL, "cannot repack a %lld x %lld tensor of type %d", (long long)rows, (long long)cols, type);
+    void *base = nullptr;
+    hipError_t e = hipMalloc(&base, L.total);
+    if (e != hipSuccess) return fail(JEV_ENOMEM, "hipMalloc(%zu) for a weight failed: %s", L.total, hipGetErrorString(e));
+    e = hipMemcpy(base, staging.data(), L.total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(base);
+        return fail(JEV_EDEVICE, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    w.type = type;
+    w.rows = (int)rows;
+    w.cols = (int)cols;
+    w.base = base;
+    w.bytes = L.total;
+    uint8_t *b8 = (uint8_t *)base;
+    w.qs = b8 + L.qs;
+    w.d = (const uint16_t *)(b8 + L.d);
+    w.m = type == kQ5_1 ? (const uint16_t *)(b8 + L.m) : nullptr;
+    w.qh = type == kQ5_1 ? (const uint32_t *)(b8 + L.qh) : nullptr;
+    return JEV_OK;
+}
+
+int upload_vector(int type, int64_t count, const void *bytes, float **dst)
+{
+    std::vector<float> v((size_t)count);
+    if (type == kF32) {
+        std::memcpy(v.data(), bytes, (size_t)count * 4);
+    } else if (type == kF16) {
+        const uint16_t *hp = (const uint16_t *)bytes;
+        for (int64_t i = 0; i < count; i++) {
+            uint16_t hv;
+            std::memcpy(&hv, hp + i, 2);
+            v[(size_t)i] = half_to_float(hv);
+        }
+    } else {
+        return fail(JEV_EDATA, "a 1-D parameter must be F32 or F16, got type %d", type);
+    }
+    if (*dst) (void)hipFree(*dst);
+    *dst = nullptr;
+    HIP_TRY(hipMalloc((void **)dst, (size_t)count * sizeof(float)));
+    HIP_TRY(hipMemcpy(*dst, v.data(), (size_t)count * sizeof(float), hipMemcpyHostToDevice));
+    return JEV_OK;
+}
+
+// KvCache.EnsureCapacity (KvCache.cs:48-70): doubles until it fits and copies
+// the populated prefix of every head.
+int kv_ensure(jev_ctx *c, int required)
+{
+    if (required <= c->cap) return JEV_OK;
+    int cap = std::max(1, c->cap);
+    while (cap < required) cap *= 2;
+    size_t heads = (size_t)c->cfg.n_layers * c->cfg.n_kv_heads;
+    size_t bytes = heads * cap * c->cfg.head_dim * sizeof(float);
+    float *k = nullptr, *v = nullptr;
+    hipError_t e = hipMalloc((void **)&k, bytes);
+    if (e == hipSuccess) e = hipMalloc((void **)&v, bytes);
+    if (e != hipSuccess) {
+        if (k) (void)hipFree(k);
+        return fail(JEV_ENOMEM, "KV cache growth to %d positions (%zu bytes x 2) failed: %s", cap, bytes,
+                    hipGetErrorString(e));
+    }
+    if (c->kc && c->len > 0) {
+        HIP_TRY(launch_kv_copy(c->kc, k, (int)heads, c->cap, cap, c->len, c->cfg.head_dim, c->stream));
+        HIP_TRY(launch_kv_copy(c->vc, v, (int)heads, c->cap, cap, c->len, c->cfg.head_dim, c->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->kc) (void)hipFree(c->kc);
+    if (c->vc) (void)hipFree(c->vc);
+    c->kc = k;
+    c->vc = v;
+    c->cap = cap;
+    return JEV_OK;
+}
+
+bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a.type == b.type && b.type == c.type; }
+
+// One linear step y = x . W^T over up to three weights sharing x.  T >= 2:
+// MFMA GEMM on the fp16 pair; T == 1: GEMV on fp32 x.
+int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xhi, const uint16_t *xlo,
+           const float *xsum, const float *x32, float *y, int ldy)
+{
+    double nrows = 0, wbytes = 0;
+    for (int i = 0; i < nw; i++) {
+        nrows += ws[i]->rows;
+        wbytes += weight_bytes(*ws[i]);
+    }
+    const double K = ws[0]->cols;
+    if (T == 1) {
+        GemvArgs g;
+        g.K = ws[0]->cols;
+        g.x = x32;
+        g.nseg = nw;
+        for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
+        g.y = y;
+        ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows));
+        HIP_TRY(launch_gemv(g, c->stream));
+        return JEV_OK;
+    }
+    ProfScope ps(c, JEV_PROF_GEMM, 2.0 * T * nrows * K, wbytes + T * (4.0 * K + 4.0 * nrows));
+    GemmArgs g;
+    g.M = T;
+    g.K = ws[0]->cols;
+    g.xhi = xhi;
+    g.xlo = xlo;
+    g.xsum = xsum;
+    g.nseg = nw;
+    for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
+    g.ldy = ldy;
+    g.y = y;
+    HIP_TRY(launch_gemm(g, c->stream));
+    return JEV_OK;
+}
+
+int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
+{
+    const jev_config &f = c->cfg;
+    size_t qkv = (size_t)c->qdim() + 2 * c->kvdim();
+    size_t wide = std::max<size_t>({(size_t)f.hidden, (size_t)c->qdim(), (size_t)f.ffn});
+    HIP_TRY(c->h.ensure((size_t)T * f.hidden));
+    HIP_TRY(c->y.ensure((size_t)T * qkv));
+    HIP_TRY(c->yo.ensure((size_t)T * f.hidden));
+    HIP_TRY(c->ydown.ensure((size_t)T * f.hidden));
+    HIP_TRY(c->q.ensure((size_t)T * c->qdim()));
+    HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + 1));
+    if (T == 1) {
+        HIP_TRY(c->x32.ensure((size_t)std::max<size_t>(f.hidden, 1)));
+        HIP_TRY(c->ctx32.ensure((size_t)c->qdim()));
+        HIP_TRY(c->f32.ensure((size_t)f.ffn));
+        HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
+    } else {
+        HIP_TRY(c->xhi.ensure((size_t)T * std::max(f.hidden, c->qdim())));
+        HIP_TRY(c->xlo.ensure((size_t)T * std::max(f.hidden, c->qdim())));
+        HIP_TRY(c->fhi.ensure((size_t)T * f.ffn));
+        HIP_TRY(c->flo.ensure((size_t)T * f.ffn));
+    }
+    size_t nx = std::max(1, n_out);
+    HIP_TRY(c->xn.ensure(nx * f.hidden));
+    if (mode == JEV_OUT_FULL || mode == JEV_OUT_LAST_FULL) {
+        HIP_TRY(c->logits.ensure(nx * (size_t)f.vocab));
+        if (nx >= 2) {
+            HIP_TRY(c->xhi.ensure(std::max(c->xhi.n, nx * f.hidden)));
+            HIP_TRY(c->xlo.ensure(std::max(c->xlo.n, nx * f.hidden)));
+        }
+    }
+    HIP_TRY(c->amax_v.ensure(512));
+    HIP_TRY(c->amax_i.ensure(512));
+    return JEV_OK;
+}
+
+struct Plan {
+    int T = 0;
+    int start = 0;
+    int end = 0;
+    bool has_layout = false;
+    int n_out = 1;
+    int max_chunks = 0;
+    // device pointers into ctx->ints
+    const int32_t *d_tokens = nullptr, *d_slot = nullptr, *d_pos = nullptr, *d_slo = nullptr, *d_shi = nullptr,
+                  *d_seg = nullptr, *d_out = nullptr, *d_rows = nullptr;
+    int n_tiles = 0;
+    double visible_pairs = 0; // sum over tokens of visible keys
+    double kv_rows = 0;       // distinct cache rows a layer's attention reads
+};
+
+// Validates a layout the way the reference's own checks would fail
+// (MinistralModel.cs:306, :202-207) plus what keeps every kernel in bounds.
+int check_layout(const jev_ctx *c, int T, const jev_layout *L)
+{
+    if (!L->slot || !L->position || !L->shared_lo || !L->shared_hi || !L->segment)
+        return fail(JEV_EINVAL, "layout arrays must not be null");
+    if (L->end <= 0 || L->end > (1 << 28)) return fail(JEV_EINVAL, "layout end %d is out of range", L->end);
+    for (int t = 0; t < T; t++) {
+        int s = L->slot[t], lo = L->shared_lo[t], hi = L->shared_hi[t], seg = L->segment[t];
+        if (s < 0 || s >= L->end) return fail(JEV_EINVAL, "token %d: slot %d outside [0, end=%d)", t, s, L->end);
+        if (lo < 0 || hi < lo || hi > L->end) return fail(JEV_EINVAL, "token %d: shared range [%d, %d) is invalid", t, lo, hi);
+        if (seg < 0 || seg > s) return fail(JEV_EINVAL, "token %d: segment %d is after its slot %d", t, seg, s);
+        if (L->position[t] < 0) return fail(JEV_EINVAL, "token %d: negative position", t);
+    }
+    if (L->n_outputs < 0 || (L->n_outputs > 0 && !L->outputs)) return fail(JEV_EINVAL, "bad outputs list");
+    for (int b = 0; b < L->n_outputs; b++)
+        if (L->outputs[b] < 0 || L->outputs[b] >= T) return fail(JEV_EINVAL, "output %d names token %d of %d", b, L->outputs[b], T);
+    return JEV_OK;
+}
+
+// Uploads tokens (unless already on the device), layout arrays, outputs,
+// selected rows and the attention tiles.
+int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, const jev_layout *L, int mode,
+               const int32_t *rows, int n_rows, Plan &p)
+{
+    p.T = T;
+    p.start = c->len;
+    p.has_layout = L != nullptr;
+    p.end = L ? L->end : c->len + T;
+    p.n_out = L ? L->n_outputs : 1;
+    if (mode == JEV_OUT_LAST_FULL) p.n_out = 1;
+
+    std::vector<int32_t> &H = c->host_ints;
+    H.clear();
+    auto push = [&](const int32_t *src, int n) {
+        size_t off = H.size();
+        if (src) H.insert(H.end(), src, src + n);
+        else H.resize(H.size() + n, 0);
+        return off;
+    };
+    size_t o_tok = push(tokens_on_device ? nullptr : tokens, T);
+    size_t o_slot = 0, o_pos = 0, o_slo = 0, o_shi = 0, o_seg = 0;
+    if (L) {
+        o_slot = push(L->slot, T);
+        o_pos = push(L->position, T);
+        o_slo = push(L->shared_lo, T);
+        o_shi = push(L->shared_hi, T);
+        o_seg = push(L->segment, T);
+    }
+    std::vector<int32_t> outs;
+    if (mode == JEV_OUT_LAST_FULL || !L) outs.push_back(T - 1);
+    else outs.assign(L->outputs, L->outputs + L->n_outputs);
+    size_t o_out = push(outs.data(), (int)outs.size());
+    size_t o_rows = push(rows, rows ? n_rows : 0);
+
+    // Attention tiles (T >= 2) and decode chunks (T == 1).
+    std::vector<AttnTile> &tiles = c->host_tiles;
+    tiles.clear();
+    int max_limit = 0;
+    for (int t = 0; t < T;) {
+        auto at = [&](int i, int &slot, int &lo, int &hi, int &seg) {
+            if (L) {
+                slot = L->slot[i];
+                lo = L->shared_lo[i];
+                hi = L->shared_hi[i];
+                seg = L->segment[i];
+            } else {
+                slot = p.start + i;
+                lo = 0;
+                hi = p.start;
+                seg = p.start;
+            }
+        };
+        int s0, lo0, hi0, seg0;
+        at(t, s0, lo0, hi0, seg0);
+        int n = 1;
+        while (n < 64 && t + n < T) {
+            int s, lo, hi, seg;
+            at(t + n, s, lo, hi, seg);
+            if (lo != lo0 || hi != hi0 || seg != seg0 || s != s0 + n) break;
+            n++;
+        }
+        AttnTile tile{t, n, lo0, hi0, seg0, s0, 0, 0};
+        tiles.push_back(tile);
+        for (int i = 0; i < n; i++) p.visible_pairs += (double)(hi0 - lo0) + (s0 + i - seg0 + 1);
+        max_limit = std::max(max_limit, (hi0 - lo0) + (s0 + n - 1 - seg0 + 1));
+        t += n;
+    }
+    p.n_tiles = (int)tiles.size();
+    p.kv_rows = std::min<double>(p.end, max_limit + (double)T);
+    p.max_chunks = (max_limit + 63) / 64;
+
+    HIP_TRY(c->ints.ensure(H.size() + 1));
+    HIP_TRY(c->tiles.ensure(tiles.size() + 1));
+    // Stage through pinned memory; wait until the previous upload has read it.
+    HIP_TRY(hipEventSynchronize(c->copied));
+    if (c->pin_ints_n < H.size() + 1) {
+        if (c->pin_ints) HIP_TRY(hipHostFree(c->pin_ints));
+        c->pin_ints = nullptr;
+        c->pin_ints_n = 0;
+        HIP_TRY(hipHostMalloc((void **)&c->pin_ints, (H.size() + 1) * sizeof(int32_t), hipHostMallocDefault));
+        c->pin_ints_n = H.size() + 1;
+    }
+    if (c->pin_tiles_n < tiles.size() + 1) {
+        if (c->pin_tiles) HIP_TRY(hipHostFree(c->pin_tiles));
+        c->pin_tiles = nullptr;
+        c->pin_tiles_n = 0;
+        HIP_TRY(hipHostMalloc((void **)&c->pin_tiles, (tiles.size() + 1) * sizeof(AttnTile), hipHostMallocDefault));
+        c->pin_tiles_n = tiles.size() + 1;
+    }
+    std::memcpy(c->pin_ints, H.data(), H.size() * sizeof(int32_t));
+    std::memcpy(c->pin_tiles, tiles.data(), tiles.size() * sizeof(AttnTile));
+    HIP_TRY(hipMemcpyAsync(c->ints.p, c->pin_ints, H.size() * sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(c->tiles.p, c->pin_tiles, tiles.size() * sizeof(AttnTile), hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipEventRecord(c->copied, c->stream));
+    int32_t *base = c->ints.p;
+    p.d_tokens = tokens_on_device ? tokens : base + o_tok;
+    if (L) {
+        p.d_slot = base + o_slot;
+        p.d_pos = base + o_pos;
+        p.d_slo = base + o_slo;
+        p.d_shi = base + o_shi;
+        p.d_seg = base + o_seg;
+    }
+    p.d_out = base + o_out;
+    p.d_rows = rows ? base + o_rows : nullptr;
+    return JEV_OK;
+}
+
+// Enqueues the whole forward pass; the head output lands in `dout`
+// (device) or in ctx->logits / ctx->xn scratch.
+int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout)
+{
+    const jev_config &f = c->cfg;
+    const int T = p.T, D = f.hidden, qdim = c->qdim(), kvdim = c->kvdim();
+    const int group = f.n_heads / f.n_kv_heads;
+    const float scale = 1.0f / sqrtf((float)f.head_dim);
+    const bool q51 = c->layers[0].q.type == kQ5_1; // per-weight below
+    (void)q51;
+    hipStream_t s = c->stream;
+
+    HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
+    for (int l = 0; l < f.n_layers; l++) {
+        if (c->cancel.exchange(0)) return fail(JEV_ECANCELED, "the forward pass was cancelled at layer %d", l);
+        const Layer &L = c->layers[l];
+        float *kc = c->kc + (size_t)l * c->layer_stride();
+        float *vc = c->vc + (size_t)l * c->layer_stride();
+
+        // attention norm (+ the previous layer's FFN residual)
+        NormArgs na;
+        na.T = T;
+        na.D = D;
+        na.h = c->h.p;
+        na.add = l > 0 ? c->ydown.p : nullptr;
+        na.w = L.attn_norm;
+        na.eps = f.rms_eps;
+        if (T == 1) na.out32 = c->x32.p;
+        else {
+            na.ohi = c->xhi.p;
+            na.olo = c->xlo.p;
+            if (L.q.type == kQ5_1) na.xsum = c->xsum.p;
+        }
+        HIP_TRY(launch_rmsnorm(na, s));
+
+        // Q | K | V
+        const int ldqkv = qdim + 2 * kvdim;
+        bool fuse = same_type3(L.q, L.k, L.v) && (T == 1 || (qdim % 128 == 0 && kvdim % 128 == 0));
+        if (fuse) {
+            const QWeight *ws[3] = {&L.q, &L.k, &L.v};
+            int rc = linear(c, T, ws, 3, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, c->y.p, ldqkv);
+            if (rc) return rc;
+        } else {
+            const QWeight *wq[1] = {&L.q}, *wk[1] = {&L.k}, *wv[1] = {&L.v};
+            float *yq = c->y.p, *yk = c->y.p + qdim, *yv = c->y.p + qdim + kvdim;
+            int rc = linear(c, T, wq, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yq, ldqkv);
+            if (!rc) rc = linear(c, T, wk, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yk, ldqkv);
+            if (!rc) rc = linear(c, T, wv, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yv, ldqkv);
+            if (rc) return rc;
+        }
+        if (T == 1 && !fuse) {
+            // GEMV writes rows contiguously; the three outputs of one token are
+            // already at their column offsets.
+        }
+
+        RopeArgs ra;
+        ra.T = T;
+        ra.n_heads = f.n_heads;
+        ra.n_kv = f.n_kv_heads;
+        ra.hd = f.head_dim;
+        ra.half = c->half;
+        ra.q_in = c->y.p;
+        ra.k_in = c->y.p + qdim;
+        ra.v_in = c->y.p + qdim + kvdim;
+        ra.ld_in = ldqkv;
+        ra.q_out = c->q.p;
+        ra.kc = kc;
+        ra.vc = vc;
+        ra.cap = c->cap;
+        ra.pos = p.d_pos;
+        ra.slot = p.d_slot;
+        ra.start = p.start;
+        ra.freqs = c->freqs;
+        ra.mscale = c->mscale;
+        ra.orig_ctx = f.rope_original_context;
+        ra.temp_scale = f.attention_temperature_scale;
+        HIP_TRY(launch_rope_store(ra, s));
+
+        if (T == 1) {
+            DecodeAttnArgs da;
+            da.T = 1;
+            da.n_heads = f.n_heads;
+            da.group = group;
+            da.hd = f.head_dim;
+            da.max_chunks = p.max_chunks;
+            da.q = c->q.p;
+            da.kc = kc;
+            da.vc = vc;
+            da.cap = c->cap;
+            da.slot = p.d_slot;
+            da.shared_lo = p.d_slo;
+            da.shared_hi = p.d_shi;
+            da.segment = p.d_seg;
+            da.start = p.start;
+            da.scale = scale;
+            da.part = c->part.p;
+            da.ctx = c->ctx32.p;
+            ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
+                         8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
+            HIP_TRY(launch_attn_decode(da, s));
+        } else {
+            AttnArgs aa;
+            aa.n_tiles = p.n_tiles;
+            aa.n_heads = f.n_heads;
+            aa.group = group;
+            aa.hd = f.head_dim;
+            aa.tiles = c->tiles.p;
+            aa.q = c->q.p;
+            aa.kc = kc;
+            aa.vc = vc;
+            aa.cap = c->cap;
+            aa.scale = scale;
+            aa.ohi = c->xhi.p;
+            aa.olo = c->xlo.p;
+            {
+                ProfScope ps(c, JEV_PROF_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
+                             8.0 * f.head_dim * f.n_kv_heads * p.kv_rows + 8.0 * T * qdim);
+                HIP_TRY(launch_attn_tree(aa, s));
+            }
+            if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xhi.p, c->xlo.p, T, qdim, c->xsum.p, s));
+        }
+        {
+            const QWeight *wo[1] = {&L.o};
+            int rc = linear(c, T, wo, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->ctx32.p, c->yo.p, D);
+            if (rc) return rc;
+        }
+
+        // FFN norm (+ attention residual)
+        NormArgs nf = na;
+        nf.add = c->yo.p;
+        nf.w = L.ffn_norm;
+        nf.xsum = (T > 1 && L.gate.type == kQ5_1) ? c->xsum.p : nullptr;
+        HIP_TRY(launch_rmsnorm(nf, s));
+
+        if (T == 1) {
+            GemvArgs g;
+            g.K = D;
+            g.x = c->x32.p;
+            g.nseg = 2;
+            g.seg[0] = L.gate;
+            g.seg[1] = L.up;
+            g.y = c->f32.p;
+            g.swiglu = 1;
+            ProfScope ps(c, JEV_PROF_GEMV, 4.0 * f.ffn * D, weight_bytes(L.gate) + weight_bytes(L.up) + 4.0 * (D + f.ffn));
+            HIP_TRY(launch_gemv(g, s));
+        } else {
+            GemmArgs g;
+            g.M = T;
+            g.K = D;
+            g.xhi = c->xhi.p;
+            g.xlo = c->xlo.p;
+            g.xsum = c->xsum.p;
+            g.nseg = 2;
+            g.seg[0] = L.gate;
+            g.seg[1] = L.up;
+            g.mode = kGemmSwiGlu;
+            g.ohi = c->fhi.p;
+            g.olo = c->flo.p;
+            ProfScope ps(c, JEV_PROF_GEMM, 4.0 * T * f.ffn * D,
+                         weight_bytes(L.gate) + weight_bytes(L.up) + T * (4.0 * D + 4.0 * f.ffn));
+            HIP_TRY(launch_gemm(g, s));
+            if (L.down.type == kQ5_1) HIP_TRY(launch_block_sums(c->fhi.p, c->flo.p, T, f.ffn, c->xsum.p, s));
+        }
+        {
+            const QWeight *wd[1] = {&L.down};
+            int rc = linear(c, T, wd, 1, c->fhi.p, c->flo.p, c->xsum.p, c->f32.p, c->ydown.p, D);
+            if (rc) return rc;
+        }
+    }
+
+    // Heads.  The last layer's FFN residual is folded into the final norm of
+    // the output rows (h itself is not needed after the last layer).
+    if (mode == JEV_OUT_NONE) return JEV_OK;
+    const QWeight &tab = c->table();
+    NormArgs fn;
+    fn.T = p.n_out;
+    fn.D = D;
+    fn.h = c->h.p;
+    fn.add = c->ydown.p;
+    fn.store_h = false;
+    fn.w = c->out_norm;
+    fn.eps = f.rms_eps;
+    fn.rows = p.d_out;
+    if (mode == JEV_OUT_SELECTED) {
+        fn.out32 = c->xn.p;
+        HIP_TRY(launch_rmsnorm(fn, s));
+        HeadRowsArgs hr;
+        hr.n_out = p.n_out;
+        hr.n_rows = n_rows;
+        hr.D = D;
+        hr.xn = c->xn.p;
+        hr.table = tab;
+        hr.rows = p.d_rows;
+        hr.out = dout;
+        HIP_TRY(launch_head_rows(hr, s));
+        return JEV_OK;
+    }
+    // full vocabulary
+    if (p.n_out == 1) {
+        fn.out32 = c->xn.p;
+        HIP_TRY(launch_rmsnorm(fn, s));
+        GemvArgs g;
+        g.K = D;
+        g.x = c->xn.p;
+        g.nseg = 1;
+        g.seg[0] = tab;
+        g.y = dout;
+        ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows));
+        HIP_TRY(launch_gemv(g, s));
+    } else {
+        fn.ohi = c->xhi.p;
+        fn.olo = c->xlo.p;
+        fn.xsum = tab.type == kQ5_1 ? c->xsum.p : nullptr;
+        HIP_TRY(launch_rmsnorm(fn, s));
+        GemmArgs g;
+        g.M = p.n_out;
+        g.K = D;
+        g.xhi = c->xhi.p;
+        g.xlo = c->xlo.p;
+        g.xsum = c->xsum.p;
+        g.nseg = 1;
+        g.seg[0] = tab;
+        g.ldy = tab.rows;
+        g.y = dout;
+        ProfScope ps(c, JEV_PROF_GEMM, 2.0 * p.n_out * tab.rows * D, weight_bytes(tab) + p.n_out * 4.0 * (D + tab.rows));
+        HIP_TRY(launch_gemm(g, s));
+    }
+    return JEV_OK;
+}
+
+size_t out_floats(const jev_ctx *c, int mode, int n_out, int n_rows)
+{
+    switch (mode) {
+    case JEV_OUT_NONE: return 0;
+    case JEV_OUT_LAST_FULL: return (size_t)c->cfg.vocab;
+    case JEV_OUT_SELECTED: return (size_t)n_out * n_rows;
+    case JEV_OUT_FULL: return (size_t)n_out * c->cfg.vocab;
+    default: return 0;
+    }
+}
+
+int check_ready(jev_ctx *c)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    if (!c->finalized) return fail(JEV_ESTATE, "jev_finalize has not succeeded on this context");
+    HIP_TRY(hipSetDevice(c->device));
+    return JEV_OK;
+}
+
+// Common front half of jev_forward / jev_forward_device.
+int prepare(jev_ctx *c, const int32_t *tokens, bool on_device, int T, const jev_layout *layout, int mode,
+            const int32_t *rows, int n_rows, Plan &p)
+{
+    if (T <= 0) return fail(JEV_EINVAL, "No tokens to forward.");
+    if (!tokens) return fail(JEV_EINVAL, "tokens is null");
+    if (mode < JEV_OUT_NONE || mode > JEV_OUT_FULL) return fail(JEV_EINVAL, "unknown output mode %d", mode);
+    if (mode == JEV_OUT_SELECTED) {
+        if (!rows || n_rows <= 0) return fail(JEV_EINVAL, "selected-rows mode needs rows");
+        for (int i = 0; i < n_rows; i++)
+            if (rows[i] < 0 || rows[i] >= c->table().rows)
+                return fail(JEV_EINVAL, "vocabulary row %d is outside the %d-row head", rows[i], c->table().rows);
+    }
+    if (!on_device)
+        for (int t = 0; t < T; t++)
+            if (tokens[t] < 0 || tokens[t] >= c->embd.rows) // QuantMatMul.GatherRows (QuantMatMul.cs:300-302)
+                return fail(JEV_EINVAL, "Token id %d is outside the %d-entry embedding table.", tokens[t], c->embd.rows);
+    if (layout) {
+        int rc = check_layout(c, T, layout);
+        if (rc) return rc;
+        if (mode == JEV_OUT_SELECTED || mode == JEV_OUT_FULL)
+            if (layout->n_outputs <= 0) return fail(JEV_EINVAL, "the layout lists no outputs");
+    }
+    int end = layout ? layout->end : c->len + T;
+    int rc = kv_ensure(c, end);
+    if (rc) return rc;
+    rc = build_plan(c, tokens, on_device, T, layout, mode, rows, n_rows, p);
+    if (rc) return rc;
+    return ensure_workspace(c, T, p.n_out, mode, p.max_chunks);
+}
+
+} // namespace
+
+// ================================================================ C ABI
+
+extern "C" {
+
+const char *jev_last_error(void) { return g_error.c_str(); }
+
+int jev_create(const jev_config *cfg, int device, jev_ctx **out)
+{
+    if (!cfg || !out) return fail(JEV_EINVAL, "null argument");
+    *out = nullptr;
+    const jev_config &f = *cfg;
+    if (f.n_layers <= 0 || f.hidden <= 0 || f.n_heads <= 0 || f.n_kv_heads <= 0 || f.ffn <= 0 || f.vocab <= 0)
+        return fail(JEV_EINVAL, "model dimensions must be positive");
+    if (f.n_heads % f.n_kv_heads != 0) // ModelConfig.FromGguf (ModelConfig.cs:108-110)
+        return fail(JEV_EDATA, "%d attention heads do not divide into %d KV heads.", f.n_heads, f.n_kv_heads);
+    if (f.head_dim != 128) return fail(JEV_EINVAL, "head_dim %d: the kernels are built for 128-wide heads", f.head_dim);
+    if (f.hidden % 32 != 0 || f.ffn % 64 != 0) return fail(JEV_EINVAL, "hidden must be a multiple of 32 and ffn of 64");
+    if (f.rope_dim <= 0 || f.rope_dim > f.head_dim || f.rope_dim % 2 != 0)
+        return fail(JEV_EINVAL, "rope_dim %d must be even and at most head_dim", f.rope_dim);
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) return fail(JEV_EDEVICE, "no HIP device: %s", hipGetErrorString(e));
+    if (device < 0 || device >= ndev) return fail(JEV_EINVAL, "device %d of %d", device, ndev);
+    HIP_TRY(hipSetDevice(device));
+    jev_ctx *c = new jev_ctx();
+    c->cfg = f;
+    c->device = device;
+    c->layers.resize(f.n_layers);
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(JEV_EDEVICE, "hipStreamCreate: %s", hipGetErrorString(e));
+    }
+    e = hipEventCreateWithFlags(&c->copied, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(c->copied, c->stream);
+    if (e != hipSuccess) {
+        jev_destroy(c);
+        return fail(JEV_EDEVICE, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    std::vector<float> freqs;
+    c->half = rope_table(f, freqs, c->mscale);
+    e = hipMalloc((void **)&c->freqs, freqs.size() * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(c->freqs, freqs.data(), freqs.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        jev_destroy(c);
+        return fail(JEV_EDEVICE, "rope table: %s", hipGetErrorString(e));
+    }
+    int rc = kv_ensure(c, std::max(1, f.initial_kv_capacity));
+    if (rc) {
+        std::string msg = g_error;
+        jev_destroy(c);
+        return fail(rc, "%s", msg.c_str());
+    }
+    *out = c;
+    return JEV_OK;
+}
+
+void jev_destroy(jev_ctx *c)
+{
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    free_weight(c->embd);
+    free_weight(c->output);
+    if (c->out_norm) (void)hipFree(c->out_norm);
+    for (auto &L : c->layers) {
+        if (L.attn_norm) (void)hipFree(L.attn_norm);
+        if (L.ffn_norm) (void)hipFree(L.ffn_norm);
+        free_weight(L.q); free_weight(L.k); free_weight(L.v); free_weight(L.o);
+        free_weight(L.gate); free_weight(L.up); free_weight(L.down);
+    }
+    if (c->freqs) (void)hipFree(c->freqs);
+    if (c->kc) (void)hipFree(c->kc);
+    if (c->vc) (void)hipFree(c->vc);
+    c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
+    c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
+    c->part.release(); c->xsum.release(); c->xhi.release(); c->xlo.release(); c->fhi.release();
+    c->flo.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    if (c->pin_ints) (void)hipHostFree(c->pin_ints);
+    if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
+    if (c->copied) (void)hipEventDestroy(c->copied);
+    for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int jev_bind_tensor(jev_ctx *c, int slot, int layer, int type, int64_t rows, int64_t cols, const void *bytes,
+                    size_t nbytes)
+{
+    if (!c || !bytes) return fail(JEV_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(c->device));
+    if (slot < JEV_SLOT_TOKEN_EMBD || slot > JEV_SLOT_DOWN) return fail(JEV_EINVAL, "unknown tensor slot %d", slot);
+    if (slot >= JEV_SLOT_ATTN_NORM && (layer < 0 || layer >= c->cfg.n_layers))
+        return fail(JEV_EINVAL, "layer %d of %d", layer, c->cfg.n_layers);
+    if (rows <= 0 || cols <= 0 || rows > INT32_MAX || cols > INT32_MAX) return fail(JEV_EINVAL, "bad shape");
+    int bs = block_size(type);
+    if (bs == 0) return fail(JEV_EDATA, "GGML type %d is not supported by this runtime", type);
+    if (cols % bs != 0) return fail(JEV_EDATA, "%lld columns are not whole blocks of %d", (long long)cols, bs);
+    size_t need = (size_t)row_bytes(type, cols) * (size_t)rows;
+    if (nbytes < need) // GgufFile.ThrowIfTruncated's concern, per tensor
+        return fail(JEV_EDATA, "tensor bytes are truncated: %zu of %zu", nbytes, need);
+    c->finalized = false;
+    bool vec = slot == JEV_SLOT_OUTPUT_NORM || slot == JEV_SLOT_ATTN_NORM || slot == JEV_SLOT_FFN_NORM;
+    if (vec) {
+        if (rows != 1) return fail(JEV_EDATA, "a norm weight must be 1-D");
+        float **dst = slot == JEV_SLOT_OUTPUT_NORM ? &c->out_norm
+                    : slot == JEV_SLOT_ATTN_NORM ? &c->layers[layer].attn_norm : &c->layers[layer].ffn_norm;
+        return upload_vector(type, cols, bytes, dst);
+    }
+    if (!is_quant(type)) return fail(JEV_EDATA, "weight matrices must be Q8_0, Q5_1 or Q4_0 (type %d)", type);
+    QWeight *w = nullptr;
+    switch (slot) {
+    case JEV_SLOT_TOKEN_EMBD: w = &c->embd; break;
+    case JEV_SLOT_OUTPUT: w = &c->output; break;
+    case JEV_SLOT_Q: w = &c->layers[layer].q; break;
+    case JEV_SLOT_K: w = &c->layers[layer].k; break;
+    case JEV_SLOT_V: w = &c->layers[layer].v; break;
+    case JEV_SLOT_O: w = &c->layers[layer].o; break;
+    case JEV_SLOT_GATE: w = &c->layers[layer].gate; break;
+    case JEV_SLOT_UP: w = &c->layers[layer].up; break;
+    case JEV_SLOT_DOWN: w = &c->layers[layer].down; break;
+    default: return fail(JEV_EINVAL, "slot %d", slot);
+    }
+    free_weight(*w);
+    return upload_weight(type, rows, cols, bytes, *w);
+}
+
+int jev_finalize(jev_ctx *c)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    const jev_config &f = c->cfg;
+    int qdim = c->qdim(), kvdim = c->kvdim();
+    if (!c->embd.base) return fail(JEV_EDATA, "missing tensor 'token_embd.weight'.");
+    if (!c->out_norm) return fail(JEV_EDATA, "missing tensor 'output_norm.weight'.");
+    // MinistralModel.ValidateShapes (MinistralModel.cs:110-123) and the rest of the shapes.
+    if (c->embd.cols != f.hidden)
+        return fail(JEV_EDATA, "token_embd is %d wide but the model's hidden size is %d.", c->embd.cols, f.hidden);
+    if (c->table().rows != f.vocab || c->table().cols != f.hidden)
+        return fail(JEV_EDATA, "the LM head is %d x %d; expected %d x %d", c->table().rows, c->table().cols, f.vocab, f.hidden);
+    for (int l = 0; l < f.n_layers; l++) {
+        Layer &L = c->layers[l];
+        const char *missing = !L.attn_norm ? "attn_norm" : !L.ffn_norm ? "ffn_norm" : !L.q.base ? "attn_q"
+                            : !L.k.base ? "attn_k" : !L.v.base ? "attn_v" : !L.o.base ? "attn_output"
+                            : !L.gate.base ? "ffn_gate" : !L.up.base ? "ffn_up" : !L.down.base ? "ffn_down" : nullptr;
+        if (missing) return fail(JEV_EDATA, "missing tensor 'blk.%d.%s.weight'.", l, missing);
+        struct { const QWeight *w; int r, c; const char *n; } chk[] = {
+            {&L.q, qdim, f.hidden, "attn_q"}, {&L.k, kvdim, f.hidden, "attn_k"}, {&L.v, kvdim, f.hidden, "attn_v"},
+            {&L.o, f.hidden, qdim, "attn_output"}, {&L.gate, f.ffn, f.hidden, "ffn_gate"},
+            {&L.up, f.ffn, f.hidden, "ffn_up"}, {&L.down, f.hidden, f.ffn, "ffn_down"}};
+        for (auto &k : chk)
+            if (k.w->rows != k.r || k.w->cols != k.c)
+                return fail(JEV_EDATA, "blk.%d.%s is %d x %d; expected %d x %d.", l, k.n, k.w->rows, k.w->cols, k.r, k.c);
+        if (L.gate.type != L.up.type) return fail(JEV_EDATA, "blk.%d: ffn_gate and ffn_up must share a type", l);
+    }
+    c->finalized = true;
+    return JEV_OK;
+}
+
+int jev_kv_length(jev_ctx *c, int32_t *length)
+{
+    if (!c || !length) return fail(JEV_EINVAL, "null argument");
+    *length = c->len;
+    return JEV_OK;
+}
+
+int jev_kv_capacity(jev_ctx *c, int32_t *capacity)
+{
+    if (!c || !capacity) return fail(JEV_EINVAL, "null argument");
+    *capacity = c->cap;
+    return JEV_OK;
+}
+
+int jev_kv_reserve(jev_ctx *c, int32_t required)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    HIP_TRY(hipSetDevice(c->device));
+    return kv_ensure(c, required);
+}
+
+int jev_kv_truncate(jev_ctx *c, int32_t length)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    c->len = std::min(std::max(length, 0), c->len); // KvCache.Truncate (KvCache.cs:46)
+    return JEV_OK;
+}
+
+int jev_kv_reset(jev_ctx *c)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    c->len = 0;
+    return JEV_OK;
+}
+
+// KvCache.Snapshot (KvCache.cs:94-112): keys of every [layer][head], then values.
+int jev_kv_snapshot(jev_ctx *c, int32_t length, float *out, size_t n)
+{
+    if (!c || !out) return fail(JEV_EINVAL, "null argument");
+    if (length < 0 || length > c->len) return fail(JEV_EINVAL, "Only %d positions are cached.", c->len);
+    const jev_config &f = c->cfg;
+    size_t per = (size_t)f.n_layers * f.n_kv_heads * length * f.head_dim;
+    if (n != per * 2) return fail(JEV_EINVAL, "Snapshot needs %zu floats; got %zu.", per * 2, n);
+    HIP_TRY(hipSetDevice(c->device));
+    size_t cur = 0, row = (size_t)length * f.head_dim;
+    for (int pass = 0; pass < 2; pass++)
+        for (int l = 0; l < f.n_layers; l++)
+            for (int h = 0; h < f.n_kv_heads; h++) {
+                const float *src = (pass ? c->vc : c->kc) + (size_t)l * c->layer_stride() + (size_t)h * c->cap * f.head_dim;
+                HIP_TRY(hipMemcpyAsync(out + cur, src, row * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+                cur += row;
+            }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return JEV_OK;
+}
+
+// KvCache.Restore (KvCache.cs:115-136): leaves the cache holding exactly that prefix.
+int jev_kv_restore(jev_ctx *c, const float *in, size_t n, int32_t length)
+{
+    if (!c || !in) return fail(JEV_EINVAL, "null argument");
+    const jev_config &f = c->cfg;
+    if (length < 0) return fail(JEV_EINVAL, "negative length");
+    size_t per = (size_t)f.n_layers * f.n_kv_heads * length * f.head_dim;
+    if (n != per * 2) return fail(JEV_EINVAL, "Snapshot holds %zu floats; %d positions need %zu.", n, length, per * 2);
+    HIP_TRY(hipSetDevice(c->device));
+    int rc = kv_ensure(c, length);
+    if (rc) return rc;
+    size_t cur = 0, row = (size_t)length * f.head_dim;
+    for (int pass = 0; pass < 2; pass++)
+        for (int l = 0; l < f.n_layers; l++)
+            for (int h = 0; h < f.n_kv_heads; h++) {
+                float *dst = (pass ? c->vc : c->kc) + (size_t)l * c->layer_stride() + (size_t)h * c->cap * f.head_dim;
+                HIP_TRY(hipMemcpyAsync(dst, in + cur, row * sizeof(float), hipMemcpyHostToDevice, c->stream));
+                cur += row;
+            }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->len = length;
+    return JEV_OK;
+}
+
+int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *layout, int mode,
+                const int32_t *rows, int32_t n_rows, float *out, size_t out_len)
+{
+    int rc = check_ready(c);
+    if (rc) return rc;
+    Plan p;
+    rc = prepare(c, tokens, false, T, layout, mode, rows, n_rows, p);
+    if (rc) return rc;
+    size_t need = out_floats(c, mode, p.n_out, n_rows);
+    if (need && (!out || out_len < need)) return fail(JEV_EINVAL, "Expected room for %zu outputs, got %zu.", need, out_len);
+    float *dout = nullptr;
+    if (need) {
+        HIP_TRY(c->logits.ensure(std::max(c->logits.n, need)));
+        dout = c->logits.p;
+    }
+    rc = enqueue_forward(c, p, mode, n_rows, dout);
+    if (rc) {
+        (void)hipStreamSynchronize(c->stream);
+        return rc;
+    }
+    if (need) HIP_TRY(hipMemcpyAsync(out, dout, need * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->len = std::max(c->len, p.end); // KvCache.Advance (MinistralModel.cs:360)
+    return JEV_OK;
+}
+
+int jev_forward_device(jev_ctx *c, const int32_t *d_tokens, int32_t T, const jev_layout *layout, int mode,
+                       const int32_t *rows, int32_t n_rows, float *d_out)
+{
+    int rc = check_ready(c);
+    if (rc) return rc;
+    Plan p;
+    rc = prepare(c, d_tokens, true, T, layout, mode, rows, n_rows, p);
+    if (rc) return rc;
+    if (out_floats(c, mode, p.n_out, n_rows) && !d_out) return fail(JEV_EINVAL, "d_out is null");
+    rc = enqueue_forward(c, p, mode, n_rows, d_out);
+    if (rc) return rc;
+    c->len = std::max(c->len, p.end);
+    return JEV_OK;
+}
+
+int jev_sync(jev_ctx *c)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return JEV_OK;
+}
+
+void *jev_stream(jev_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+// ForwardTreeAsync (MinistralModel.cs:198-219) with TokenLayout.Tree (:720-745).
+int jev_forward_tree(jev_ctx *c, const int32_t *trunk, int32_t n_trunk, const int32_t *btok, const int32_t *blen,
+                     int32_t nb, const int32_t *rows, int32_t n_rows, float *out, size_t out_len)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    if (nb <= 0 || !blen || !btok) return fail(JEV_EINVAL, "No branches to forward.");
+    if (n_trunk < 0 || (n_trunk > 0 && !trunk)) return fail(JEV_EINVAL, "bad trunk");
+    std::vector<int32_t> offsets(nb);
+    int total = n_trunk;
+    for (int b = 0; b < nb; b++) {
+        if (blen[b] <= 0) return fail(JEV_EINVAL, "Branch %d is empty.", b);
+        offsets[b] = total;
+        total += blen[b];
+    }
+    std::vector<int32_t> tokens(total), slot(total), pos(total), lo(total, 0), sh(total), seg(total), outs(nb);
+    std::copy(trunk, trunk + n_trunk, tokens.begin());
+    std::copy(btok, btok + (total - n_trunk), tokens.begin() + n_trunk);
+    int start = c->len, branch = -1;
+    for (int t = 0; t < total; t++) {
+        slot[t] = start + t;
+        while (branch + 1 < nb && t >= offsets[branch + 1]) branch++;
+        if (t < n_trunk || branch < 0) {
+            pos[t] = start + t;
+            sh[t] = start;
+            seg[t] = start;
+        } else {
+            pos[t] = start + n_trunk + (t - offsets[branch]);
+            sh[t] = start + n_trunk;
+            seg[t] = start + offsets[branch];
+        }
+    }
+    for (int b = 0; b < nb; b++) outs[b] = (b + 1 < nb ? offsets[b + 1] : total) - 1;
+    jev_layout L{slot.data(), pos.data(), lo.data(), sh.data(), seg.data(), outs.data(), nb, start + total};
+    return jev_forward(c, tokens.data(), total, &L, JEV_OUT_SELECTED, rows, n_rows, out, out_len);
+}
+
+int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *tokens_out)
+{
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (n_steps <= 0 || !tokens_out) return fail(JEV_EINVAL, "bad arguments");
+    if (first < 0 || first >= c->embd.rows) return fail(JEV_EINVAL, "Token id %d is outside the embedding table.", first);
+    DevBuf<int32_t> ids;
+    HIP_TRY(ids.ensure((size_t)n_steps + 1));
+    HIP_TRY(hipMemcpyAsync(ids.p, &first, sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    for (int i = 0; i < n_steps; i++) {
+        Plan p;
+        rc = prepare(c, ids.p + i, true, 1, nullptr, JEV_OUT_LAST_FULL, nullptr, 0, p);
+        if (!rc) rc = c->logits.ensure(std::max(c->logits.n, (size_t)c->cfg.vocab)) == hipSuccess ? JEV_OK
+                                                                                               : fail(JEV_ENOMEM, "logits");
+        if (!rc) rc = enqueue_forward(c, p, JEV_OUT_LAST_FULL, 0, c->logits.p);
+        if (rc) {
+            (void)hipStreamSynchronize(c->stream);
+            ids.release();
+            return rc;
+        }
+        c->len = std::max(c->len, p.end);
+        hipError_t e = launch_argmax(c->logits.p, c->cfg.vocab, ids.p + i + 1, c->amax_v.p, c->amax_i.p, c->stream);
+        if (e != hipSuccess) {
+            ids.release();
+            return fail(JEV_EDEVICE, "argmax: %s", hipGetErrorString(e));
+        }
+    }
+    hipError_t e = hipMemcpyAsync(tokens_out, ids.p + 1, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    ids.release();
+    if (e != hipSuccess) return fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+    return JEV_OK;
+}
+
+int jev_margins(const float *v, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature, float *margins,
+                float *probs)
+{
+    if (!v || !margins || !probs || n_options <= 0 || n_yes <= 0 || n_no <= 0)
+        return fail(JEV_EINVAL, "bad arguments");
+    int nr = n_yes + n_no;
+    for (int i = 0; i < n_options; i++) {
+        const float *r = v + (size_t)i * nr;
+        float by = r[0], bn = r[n_yes];
+        for (int j = 1; j < n_yes; j++) by = std::max(by, r[j]);
+        for (int j = 1; j < n_no; j++) bn = std::max(bn, r[n_yes + j]);
+        margins[i] = by - bn;
+        probs[i] = margins[i] / temperature;
+    }
+    // Kernels.Softmax (Kernels.cs:102-121)
+    float mx = probs[0];
+    for (int i = 1; i < n_options; i++) mx = std::max(mx, probs[i]);
+    if (!std::isfinite(mx)) {
+        for (int i = 0; i < n_options; i++) probs[i] = 1.0f / (float)n_options;
+        return JEV_OK;
+    }
+    float sum = 0.f;
+    for (int i = 0; i < n_options; i++) {
+        probs[i] = expf(probs[i] - mx);
+        sum += probs[i];
+    }
+    for (int i = 0; i < n_options; i++) probs[i] = probs[i] / sum;
+    return JEV_OK;
+}
+
+int jev_profile_enable(jev_ctx *c, int enable)
+{
+    if (!c) return fail(JEV_EINVAL, "null context");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->prof.clear();
+    c->ev_used = 0;
+    c->profiling = enable != 0;
+    return JEV_OK;
+}
+
+int jev_profile_read(jev_ctx *c, int cls, int64_t *launches, double *total_ms, double *flops, double *bytes)
+{
+    if (!c || cls < 0 || cls >= JEV_PROF_CLASSES) return fail(JEV_EINVAL, "bad arguments");
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    int64_t n = 0;
+    double ms = 0, fl = 0, by = 0;
+    for (auto &r : c->prof) {
+        if (r.cls != cls || !r.a || !r.b) continue;
+        float e = 0.f;
+        HIP_TRY(hipEventElapsedTime(&e, r.a, r.b));
+        n++;
+        ms += e;
+        fl += r.flops;
+        by += r.bytes;
+    }
+    if (launches) *launches = n;
+    if (total_ms) *total_ms = ms;
+    if (flops) *flops = fl;
+    if (bytes) *bytes = by;
+    return JEV_OK;
+}
+
+void jev_cancel(jev_ctx *c)
+{
+    if (c) c->cancel.store(1);
+}
+
+// ---------------------------------------------------------------- test hooks
+
+int jev_dequantize(int type, const void *src, size_t nbytes, float *dst, int64_t count)
+{
+    if (!src || !dst || count <= 0) return fail(JEV_EINVAL, "bad arguments");
+    if (!is_quant(type)) return fail(JEV_EINVAL, "type %d is not a block type", type);
+    if (count % 32 != 0) return fail(JEV_EINVAL, "%d decodes whole blocks of 32; asked for %lld elements.", type, (long long)count);
+    if ((int64_t)nbytes < row_bytes(type, count)) return fail(JEV_EINVAL, "need %lld bytes", (long long)row_bytes(type, count));
+    QWeight w;
+    int rc = upload_weight(type, 1, count, src, w);
+    if (rc) return rc;
+    float *d = nullptr;
+    hipError_t e = hipMalloc((void **)&d, (size_t)count * sizeof(float));
+    if (e == hipSuccess) e = launch_dequant(w, d, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(dst, d, (size_t)count * sizeof(float), hipMemcpyDeviceToHost);
+    if (d) (void)hipFree(d);
+    free_weight(w);
+    if (e != hipSuccess) return fail(JEV_EDEVICE, "dequantize: %s", hipGetErrorString(e));
+    return JEV_OK;
+}
+
+int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const float *x, int32_t tokens, float *y)
+{
+    if (!wbytes || !x || !y || tokens <= 0 || rows <= 0 || cols <= 0) return fail(JEV_EINVAL, "bad arguments");
+    if (!is_quant(type) || cols % 32 != 0) return fail(JEV_EINVAL, "unsupported type or shape");
+    QWeight w;
+    int rc = upload_weight(type, rows, cols, wbytes, w);
+    if (rc) return rc;
+    size_t nx = (size_t)tokens * cols, ny = (size_t)tokens * rows;
+    float *dx = nullptr, *dy = nullptr, *dsum = nullptr;
+    uint16_t *hi = nullptr, *lo = nullptr;
+    hipError_t e = hipMalloc((void **)&dx, nx * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess && tokens >= 2) {
+        e = hipMalloc((void **)&hi, nx * 2);
+        if (e == hipSuccess) e = hipMalloc((void **)&lo, nx * 2);
+        if (e == hipSuccess) e = hipMalloc((void **)&dsum, (nx / 32 + 1) * sizeof(float));
+        if (e == hipSuccess) e = launch_split(dx, nx, hi, lo, nullptr);
+        if (e == hipSuccess && type == kQ5_1) e = launch_block_sums(hi, lo, tokens, (int)cols, dsum, nullptr);
+        if (e == hipSuccess) {
+            GemmArgs g;
+            g.M = tokens;
+            g.K = (int)cols;
+            g.xhi = hi;
+            g.xlo = lo;
+            g.xsum = dsum;
+            g.seg[0] = w;
+            g.ldy = (int)rows;
+            g.y = dy;
+            e = launch_gemm(g, nullptr);
+        }
+    } else if (e == hipSuccess) {
+        GemvArgs g;
+        g.K = (int)cols;
+        g.x = dx;
+        g.seg[0] = w;
+        g.y = dy;
+        e = launch_gemv(g, nullptr);
+    }
+    if (e == hipSuccess) e = hipMemcpy(y, dy, ny * sizeof(float), hipMemcpyDeviceToHost);
+    for (void *pp : {(void *)dx, (void *)dy, (void *)dsum, (void *)hi, (void *)lo})
+        if (pp) (void)hipFree(pp);
+    free_weight(w);
+    if (e != hipSuccess) return fail(JEV_EDEVICE, "matmul: %s", hipGetErrorString(e));
+    return JEV_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,93 @@
+"""GPU parity of the HIP kernels through the C ABI test hooks, against the
+oracle and the golden fixtures.  Tolerances: dequantisation bit-exact; the
+quantized products at Numeric.Close 1e-4 (the bar of PanelGemmTests.cs:38-59)
+against the oracle's float32 chain; batch invariance bitwise.
+"""
+import numpy as np
+import pytest
+
+import jev
+from helpers import quant_fixtures, worst_close
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+FIX = quant_fixtures()
+
+
+def dequant_gpu(t, raw, count):
+    import ctypes
+    out = np.empty(count, np.float32)
+    b = np.ascontiguousarray(raw, dtype=np.uint8)
+    jev._lib.check(jev.lib().jev_dequantize(t, b.ctypes.data_as(ctypes.c_void_p), b.nbytes,
+                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), count))
+    return out
+
+
+def matmul_gpu(t, raw, rows, cols, x, tokens):
+    import ctypes
+    y = np.empty(tokens * rows, np.float32)
+    xx = np.ascontiguousarray(x, np.float32)
+    b = np.ascontiguousarray(raw, dtype=np.uint8)
+    F = ctypes.POINTER(ctypes.c_float)
+    jev._lib.check(jev.lib().jev_matmul_q(t, b.ctypes.data_as(ctypes.c_void_p), rows, cols, xx.ctypes.data_as(F),
+                                          tokens, y.ctypes.data_as(F)))
+    return y.reshape(tokens, rows)
+
+
+@pytest.mark.parametrize("name", ["Q4_0", "Q5_1", "Q8_0"])
+@pytest.mark.parametrize("kind", ["quantized", "synthetic"])
+def test_gpu_dequant_fixture_bit_exact(gpu, name, kind):
+    t, entry = FIX[name]
+    raw, expected = entry[kind]
+    got = dequant_gpu(t, raw, expected.size)
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+def test_gpu_dequant_random_blocks_bit_exact(gpu, t):
+    # Random bytes with finite fp16 scales: the whole encoding space.
+    rng = np.random.default_rng(t)
+    ts = {2: 18, 7: 24, 8: 34}[t]
+    raw = rng.integers(0, 256, size=(4096, ts), dtype=np.uint8)
+    raw[:, 1] &= 0x3B  # keep d (and m) finite and moderate
+    if t == jev.TYPE_Q5_1:
+        raw[:, 3] &= 0x3B
+    raw = raw.reshape(-1)
+    exp = oracle.dequantize(t, raw, 4096 * 32)
+    got = dequant_gpu(t, raw, 4096 * 32)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+SHAPES = [(128, 256, 1), (64, 3072, 5), (128, 3072, 13), (64, 4096, 6), (64, 9216, 7), (256, 512, 2),
+          (384, 1024, 130), (3072, 3072, 256), (1024, 3072, 1)]
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+@pytest.mark.parametrize("rows,cols,tokens", SHAPES)
+def test_gpu_matmul_matches_oracle(gpu, t, rows, cols, tokens):
+    rng = np.random.default_rng(rows * 7 + cols + tokens)
+    raw = jev.synth_tensor(f"w{rows}x{cols}", t, rows, cols, 0.02, seed=tokens)
+    x = rng.standard_normal((tokens, cols)).astype(np.float32)
+    exp = oracle.matmul(t, raw, rows, cols, x, tokens)
+    got = matmul_gpu(t, raw, rows, cols, x, tokens)
+    assert worst_close(exp, got) <= 1e-4, (t, rows, cols, tokens)
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+def test_gpu_matmul_batch_invariance_bitwise(gpu, t):
+    # A token's result does not depend on its batch (PanelGemmTests.cs:61-74),
+    # across the M tile boundary (128) too.
+    rows, cols = 384, 3072
+    raw = jev.synth_tensor("inv", t, rows, cols)
+    x = np.random.default_rng(1).standard_normal((300, cols)).astype(np.float32)
+    full = matmul_gpu(t, raw, rows, cols, x, 300)
+    part = matmul_gpu(t, raw, rows, cols, x[120:137], 17)
+    assert np.array_equal(full[120:137], part)
+    again = matmul_gpu(t, raw, rows, cols, x, 300)
+    assert np.array_equal(full, again)
+
+
+def test_gpu_matmul_rejects_bad_shapes(gpu):
+    raw = jev.synth_tensor("bad", jev.TYPE_Q8_0, 64, 64)
+    with pytest.raises(jev.ArgumentError):
+        matmul_gpu(jev.TYPE_Q8_0, raw, 64, 48, np.zeros((2, 48), np.float32), 2)

@@ -1,0 +1,209 @@
+"""GPU parity of the whole token loop against the oracle, and the reference's
+bitwise contracts run on the GPU.
+
+Bars (the task's tolerances against the managed CPU path):
+  logits            Numeric.Close <= 1e-3 (|g - e| / max(1, |e|))
+  verdict z         <= 2e-2 absolute
+  tree pass         bit-identical to each branch run alone after the prefix
+                    (DeciderTests.cs:55-91), and to branches off a cached prefix
+  cached prefix     bit-identical to the whole prompt (SystemPromptCacheTests.cs:42-68)
+"""
+import numpy as np
+import pytest
+
+import jev
+from helpers import rel_l2, tiny_config, worst_close
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ROWS = [13059 % 2048, 2649 % 2048, 77]
+
+
+@pytest.fixture(scope="module")
+def synth():
+    return jev.SynthModel(tiny_config(), jev.TYPE_Q8_0)
+
+
+@pytest.fixture(scope="module")
+def model(gpu, synth):
+    m = synth.open(0)
+    yield m
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def ref(synth):
+    return oracle.OracleModel(synth.config).bind_synth(synth)
+
+
+def fresh(m):
+    m.reset_kv_cache()
+    return m
+
+
+@pytest.mark.parametrize("n", [2, 37, 64, 65, 200])
+def test_causal_prefill_logits(model, ref, n):
+    tokens = jev.random_tokens(n, 2048, n)
+    g = fresh(model).forward(tokens)
+    e = fresh(ref).forward(tokens)
+    assert worst_close(e, g) <= 1e-3 and rel_l2(e, g) <= 1e-4
+    assert model.cached_token_count == n
+
+
+def test_prefill_then_decode_steps(model, ref):
+    tokens = jev.random_tokens(50, 2048, 3)
+    fresh(model).prefill(tokens[:45])
+    fresh(ref).prefill(tokens[:45])
+    for t in tokens[45:]:
+        g = model.forward([t])
+        e = ref.forward([t])
+        assert worst_close(e, g) <= 1e-3
+    assert model.cached_token_count == 50
+
+
+def test_tree_verdicts_match_oracle(model, ref):
+    trunk = jev.random_tokens(100, 2048, 5)
+    branches = [jev.random_tokens(n, 2048, 50 + n) for n in (48, 17, 1, 64, 70)]
+    g = np.array(fresh(model).forward_tree(trunk, branches, ROWS))
+    e = np.array(fresh(ref).forward_tree(trunk, branches, ROWS))
+    assert worst_close(e, g) <= 1e-3
+    zg, ze = g[:, 0] - g[:, 1], e[:, 0] - e[:, 1]
+    assert np.max(np.abs(zg - ze)) <= 2e-2
+    mg, pg = jev.margins(g[:, :2], 1, 1)
+    me, pe = oracle.margins(e[:, :2], 1, 1)
+    assert np.max(np.abs(mg - me)) <= 2e-2
+
+
+def test_tree_equals_branches_alone_bitwise(model):
+    prefix = jev.random_tokens(150, 2048, 8)
+    branches = [jev.random_tokens(n, 2048, 80 + n) for n in (48, 20, 2, 66)]
+    m = fresh(model)
+    m.prefill(prefix)
+    alone = []
+    for b in branches:
+        m.kv_truncate(len(prefix))
+        alone.append(m.forward_selected(b, ROWS))
+    tree = fresh(m).forward_tree(prefix, branches, ROWS)
+    fresh(m).prefill(prefix)
+    cached = m.forward_branches(branches, ROWS)
+    for b in range(len(branches)):
+        assert np.array_equal(alone[b], tree[b]), b
+        assert np.array_equal(alone[b], cached[b]), b
+
+
+def test_cached_prefix_equals_whole_prompt_bitwise(model):
+    tokens = jev.random_tokens(120, 2048, 9)
+    m = fresh(model)
+    whole = m.forward(tokens)
+    fresh(m).prefill(tokens[:70])
+    snap = m.kv_snapshot(70)
+    fresh(m).kv_restore(snap, 70)
+    part = m.forward(tokens[70:])
+    assert np.array_equal(whole, part)
+
+
+def test_kv_snapshot_matches_oracle_cache(model, ref):
+    tokens = jev.random_tokens(90, 2048, 10)  # initial capacity 64: grows once
+    fresh(model).prefill(tokens[:40])
+    model.prefill(tokens[40:])
+    fresh(ref).prefill(tokens)
+    g = model.kv_snapshot(90)
+    e = ref.kv_snapshot(90)
+    assert worst_close(e, g) <= 1e-3
+    assert model.kv_capacity >= 90
+
+
+def test_forward_tree_logits_full_vocab(model, ref):
+    trunk = jev.random_tokens(10, 2048, 12)
+    branches = [jev.random_tokens(3, 2048, 13), jev.random_tokens(2, 2048, 14)]
+    g = fresh(model).forward_tree_logits(trunk, branches)
+    lay_ref = fresh(ref)
+    # oracle: the same layout through forward_layout
+    offsets, total = [10, 13], 15
+    tree = jev.TokenLayout.tree(0, 10, offsets, total).with_outputs(list(range(10, 15)))
+    flat = lay_ref.forward_layout(np.concatenate([trunk] + branches), tree, oracle.OUT_FULL).reshape(5, 2048)
+    got = np.array([x for b in g for x in b])
+    assert worst_close(flat, got) <= 1e-3
+
+
+def test_rows_layout_batched_decode(model, ref):
+    # ForwardRowsAsync: independent rows after a shared prefix, one token each.
+    shared = jev.random_tokens(20, 2048, 15)
+    fresh(model).prefill(shared)
+    fresh(ref).prefill(shared)
+    rows_tok = [[5], [9], [1000]]
+    g = model.forward_rows(20, [64, 96, 128], [0, 0, 0], rows_tok, ROWS)
+    lay = jev.TokenLayout.rows(20, [64, 96, 128], [0, 0, 0], [1, 1, 1])
+    e = ref.forward_layout([5, 9, 1000], lay, oracle.OUT_SELECTED, ROWS).reshape(3, len(ROWS))
+    assert worst_close(e, np.array(g)) <= 1e-3
+
+
+def test_greedy_decode_follows_oracle(model, ref):
+    tokens = jev.random_tokens(30, 2048, 16)
+    fresh(model).prefill(tokens)
+    fresh(ref).prefill(tokens)
+    out = model.decode_greedy(int(tokens[-1]), 8)
+    # teacher-force the oracle on the GPU's choices: each must be the oracle's
+    # argmax up to the logits tolerance
+    nxt = int(tokens[-1])
+    for tok in out:
+        e = ref.forward([nxt])
+        assert e[tok] >= e.max() - 2e-3
+        nxt = int(tok)
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1])
+def test_other_block_types(gpu, t):
+    synth = jev.SynthModel(tiny_config(), t)
+    m = synth.open(0)
+    r = oracle.OracleModel(synth.config).bind_synth(synth)
+    tokens = jev.random_tokens(70, 2048, 17)
+    assert worst_close(r.forward(tokens), m.forward(tokens)) <= 1e-3
+    trunk, branches = tokens[:40], [jev.random_tokens(n, 2048, n) for n in (5, 9)]
+    g = np.array(fresh(m).forward_tree(trunk, branches, ROWS))
+    e = np.array(fresh(r).forward_tree(trunk, branches, ROWS))
+    assert np.max(np.abs((g[:, 0] - g[:, 1]) - (e[:, 0] - e[:, 1]))) <= 2e-2
+    fresh(m).prefill(tokens[:60])
+    fresh(r).prefill(tokens[:60])
+    assert worst_close(r.forward(tokens[60:61]), m.forward(tokens[60:61])) <= 1e-3
+    m.close()
+
+
+# ---------------------------------------------------------------- error paths
+
+def test_errors_match_reference_exceptions(model):
+    m = fresh(model)
+    with pytest.raises(jev.ArgumentError):
+        m.forward([])
+    with pytest.raises(jev.ArgumentError):
+        m.forward([2048])  # outside the embedding table
+    with pytest.raises(jev.ArgumentError):
+        m.forward_branches([[1], []], ROWS)
+    with pytest.raises(jev.ArgumentError):
+        m.forward_selected([1, 2], [5000])
+    with pytest.raises(jev.ArgumentError):
+        m.kv_snapshot(5)
+    assert m.cached_token_count == 0
+
+
+def test_cancel_between_layers(model):
+    m = fresh(model)
+    m.cancel()
+    with pytest.raises(jev.CancelledError):
+        m.forward([1, 2, 3])
+    assert m.cached_token_count == 0
+    m.forward([1, 2, 3])  # the flag clears
+    assert m.cached_token_count == 3
+
+
+def test_finalize_requires_every_tensor(gpu, synth):
+    m = jev.MinistralModel(synth.config)
+    with pytest.raises(jev.JevError):
+        m.forward([1])
+    with pytest.raises(jev.DataError):
+        m.finalize()
+    t = synth.tensors["token_embd.weight"]
+    with pytest.raises(jev.DataError):
+        m.bind(t.slot, t.layer, t.ggml_type, t.rows, t.cols, t.data[:-1])  # truncated
+    m.close()
