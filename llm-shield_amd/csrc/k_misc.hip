@@ -240,13 +240,15 @@ __device__ __forceinline__ void better(float &v, int &i, float v2, int i2)
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, float *ov, int32_t *oi)
+// xi == nullptr: candidates are x[k] at index k; otherwise (x[k], xi[k]) pairs
+// from the first pass.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *x, const int32_t *xi, int n, float *ov, int32_t *oi)
 {
     __shared__ float sv[256];
     __shared__ int si[256];
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int k = blockIdx.x * 256 + threadIdx.x; k < n; k += gridDim.x * 256) better(v, idx, x[k], k);
+    for (int k = blockIdx.x * 256 + threadIdx.x; k < n; k += gridDim.x * 256) better(v, idx, x[k], xi ? xi[k] : k);
     sv[threadIdx.x] = v;
     si[threadIdx.x] = idx;
     __syncthreads();
@@ -271,8 +273,9 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *x, int n, floa
 hipError_t launch_argmax(const float *x, int n, int32_t *result, float *sv, int32_t *si, hipStream_t s)
 {
     const int blocks = 256;
-    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, x, n, sv, si);
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, s, (const float *)sv, blocks, sv + blocks, si + blocks);
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, x, (const int32_t *)nullptr, n, sv, si);
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, s, (const float *)sv, (const int32_t *)si, blocks,
+                       sv + blocks, si + blocks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return hipMemcpyAsync(result, si + blocks, sizeof(int32_t), hipMemcpyDeviceToDevice, s);
