@@ -61,7 +61,8 @@ hipError_t launch_dequant(const QWeight &w, float *dst, hipStream_t s);
 // Embedding gather: h[t] = decode(row ids[t]).
 hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, hipStream_t s);
 
-// GEMM y = x . W^T with x given as an fp16 hi/lo pair (x ~= hi + lo) and W
+// GEMM y = x . W^T with x given as an fp16 hi/lo pair (x ~= hi + lo) in the
+// operand-tile layout (xt_index in jev_dev.h; rows padded to 16) and W
 // quantized.  Every output is computed in an order that does not depend on M.
 enum GemmMode : int {
     kGemmStore = 0,  // y fp32 [M][ldy]   (ldy = total columns of all segments)
@@ -69,14 +70,14 @@ enum GemmMode : int {
 };
 struct GemmArgs {
     int M = 0, K = 0;
-    const uint16_t *xhi = nullptr, *xlo = nullptr; // fp16 bits [M][K]
+    const uint16_t *xt = nullptr;                  // fp16 pair, operand-tile layout
     const float *xsum = nullptr;                   // Q5_1 only: per-32 block sums [M][K/32]
     int nseg = 1;
     QWeight seg[3];
     int ldy = 0;
     float *y = nullptr;
     int ksplit = 1;                      // fixed per (N, K); partials at y + z*M*ldy
-    uint16_t *ohi = nullptr, *olo = nullptr; // SwiGLU output, ld = seg[0].rows
+    uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
     int mode = kGemmStore;
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
@@ -97,8 +98,8 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 
 // Row kernels.
 //  rmsnorm: if add != nullptr, h[t] += add[t] first (stored back).  Output is
-//  either fp32 (out32) or an fp16 hi/lo pair; xsum (optional) receives per-32
-//  block sums of the normalised row.
+//  fp32 (out32) and/or an fp16 pair in the operand-tile layout (ot); xsum
+//  (optional) receives per-32 block sums of the normalised row.
 struct NormArgs {
     int T = 0, D = 0;
     float *h = nullptr;
@@ -108,16 +109,16 @@ struct NormArgs {
     float eps = 1e-5f;
     const int32_t *rows = nullptr; // optional row indices into h (output rows)
     float *out32 = nullptr;
-    uint16_t *ohi = nullptr, *olo = nullptr;
+    uint16_t *ot = nullptr;
     float *xsum = nullptr;
 };
 hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s);
 
-// x -> (hi, lo) fp16 pair.
-hipError_t launch_split(const float *x, size_t n, uint16_t *hi, uint16_t *lo, hipStream_t s);
+// x [T][D] fp32 -> fp16 pair in the operand-tile layout.
+hipError_t launch_split(const float *x, int T, int D, uint16_t *xt, hipStream_t s);
 
-// Per-32 block sums of an fp16 hi/lo activation (Q5_1 offset term).
-hipError_t launch_block_sums(const uint16_t *hi, const uint16_t *lo, int T, int D, float *xsum, hipStream_t s);
+// Per-32 block sums of an operand-tile activation (Q5_1 offset term).
+hipError_t launch_block_sums(const uint16_t *xt, int T, int D, float *xsum, hipStream_t s);
 
 // RoPE + KV store: y is [T][qdim + 2*kvdim] (q | k | v) or separate pointers.
 struct RopeArgs {
@@ -148,7 +149,7 @@ struct AttnArgs {
     const float *kc = nullptr, *vc = nullptr; // layer base [kvh][cap][hd]
     int cap = 0;
     float scale = 0.f;
-    uint16_t *ohi = nullptr, *olo = nullptr; // [T][qdim]
+    uint16_t *ot = nullptr; // context pair, operand-tile layout, K = qdim
 };
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 

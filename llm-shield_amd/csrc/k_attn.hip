@@ -153,19 +153,20 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
     }
 
     if (q_ok) {
+        // dims 16 j + 4 (lane/16) + r: four consecutive k, one 8-byte store per part
         float inv = 1.0f / l_run;
-        size_t base = (size_t)(tile.t0 + qi) * qdim + head * 128;
+        const int t = tile.t0 + qi, nblk = qdim >> 5;
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < 8; j++) {
+            int k = head * 128 + 16 * j + 4 * (lane >> 4);
+            uint16_t hi[4], lo[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int d = 16 * j + 4 * (lane >> 4) + r;
-                float v = o[j][r] * inv;
-                uint16_t hi, lo;
-                split_f16(v, hi, lo);
-                a.ohi[base + d] = hi;
-                a.olo[base + d] = lo;
-            }
+            for (int r = 0; r < 4; r++) split_f16(o[j][r] * inv, hi[r], lo[r]);
+            *(uint2 *)(a.ot + xt_index(t, k, nblk, 0)) =
+                make_uint2((uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16));
+            *(uint2 *)(a.ot + xt_index(t, k, nblk, 1)) =
+                make_uint2((uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16));
+        }
     }
 }
 

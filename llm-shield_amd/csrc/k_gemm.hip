@@ -5,32 +5,41 @@
 // Numerics.  The weight quants are small integers (Q8_0 q in [-127,127],
 // Q4_0 q-8 in [-8,7], Q5_1 q in [0,31]) and therefore exact in fp16; only the
 // per-32 block scale d (and Q5_1's min m) is not.  One MFMA of 16x16x32 covers
-// exactly one quant block, so each block's partial dot of x with the integer
-// quants comes out of the matrix core exactly-scaled-free and the fp32 scale is
-// applied on the vector ALU:  acc += d * (x . q)  (+ m * sum(x) for Q5_1).
-// The activation x enters as an fp16 pair hi + lo (two MFMAs into the same
-// partial), which carries ~22 significant bits; a single fp16 or bf16 operand
-// measured 4e-3 / 2e-2 relative error on the 26-layer logits, the pair 3e-5.
+// exactly one quant block, so each block's dot of x with the integer quants
+// comes out of the matrix core unscaled and the fp32 scale is applied on the
+// vector ALU:  acc += d * (x . q)  (+ m * sum(x) for Q5_1).  The activation x
+// enters as an fp16 pair hi + lo (two MFMAs into the same partial), ~22
+// significant bits; a single fp16 or bf16 operand measured 4e-3 / 2e-2
+// relative error on the 26-layer logits, the pair 3e-5.
 //
 // Determinism.  Each output is the same sequence of MFMAs and FMAs over its K
-// blocks whatever M is and whichever tile its row lands in, so a token's
-// result does not depend on the batch around it (the reference's batch
-// invariance, PanelGemm.cs:28-31); that is what keeps a tree pass bit-identical
-// to running its branches one at a time.
+// blocks whatever M is and whichever tile shape or position its row lands in,
+// so a token's result does not depend on the batch around it (the reference's
+// batch invariance, PanelGemm.cs:28-31); that is what keeps a tree pass
+// bit-identical to running its branches one at a time.  Tile shapes may
+// therefore be chosen by M without changing a single bit.
 //
-// Tiling.  256 threads = 4 waves as 2 x 2; workgroup tile 128 x 128, wave tile
-// 64 x 64 = 4 x 4 MFMA tiles; one quant block (K = 32) per pipeline step,
-// double-buffered in LDS.  The loader decodes quants to fp16 on their way into
-// LDS ("dequant in LDS"), so each decoded weight feeds all 128 rows of the
-// tile.  LDS rows are padded to 40 halves (80 bytes) so the 16-byte fragment
-// reads of 8 consecutive lanes fall on distinct banks.
+// Pipeline.  K advances 64 (two quant blocks) per stage.  Weights stream from
+// HBM as raw quant bytes into registers two stages ahead, are decoded to fp16
+// integers into a double-buffered LDS tile one stage ahead ("dequant in LDS":
+// each decoded weight feeds every row of the tile), and the activation
+// fragments are loaded straight from global memory (L2-resident) into the
+// MFMA operand registers one stage ahead.  One barrier per stage.
+//
+// Tiles.  4 waves.  Large M: 128 x 128 (waves 4 x 1, each 32 x 128 = 2 x 8
+// MFMA tiles); small M: 64 x 64 (waves 2 x 2, each 32 x 32) for parallelism.
+// Workgroup ids are remapped so each XCD (ids round-robin over 8) works on a
+// contiguous run of a grouped tile order: neighbouring tiles on one XCD share
+// weight and activation tiles in its L2.  LDS rows are padded to 72 halves
+// (144 B) so 16-byte fragment reads of 8 lanes hit distinct banks.
 #include "jev_dev.h"
 
 namespace jev {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, LDS_ROW = 40;
+constexpr int BK = 64;           // K per stage (two quant blocks)
+constexpr int LROW = BK + 8;     // padded LDS row, halves
 
 struct alignas(16) u32x4 {
     uint32_t x, y, z, w;
@@ -39,28 +48,28 @@ struct alignas(16) u32x4 {
 __device__ __forceinline__ uint16_t h16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return (uint32_t)h16(a) | ((uint32_t)h16(b) << 16); }
 
-template <int TYPE>
-struct BRaw {
-    u32x4 q;      // 16 bytes of quants
-    uint32_t qh;  // Q5_1 fifth bits
-    float d, m;   // scale, min
+// One loader chunk: 16 bytes of quants (Q8_0: 16 elements = half a block;
+// Q4_0/Q5_1: one whole block of 32) plus its block's scale fields.
+struct BChunk {
+    u32x4 q;
+    uint32_t qh;
+    uint16_t d, m;
     bool valid;
 };
 
-// Source row of the B tile's LDS row rr.
-struct RowMap {
-    const QWeight *w;
-    int row;
+template <int TYPE>
+struct Geo {
+    static constexpr int CH = TYPE == kQ8_0 ? 4 : 2; // chunks per row per stage
+    static constexpr int EL = TYPE == kQ8_0 ? 16 : 32; // elements per chunk
 };
 
-template <int MODE>
-__device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, int &seg, int &row, int &col_base)
+template <int MODE, int BN>
+__device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, int &seg, int &row)
 {
     if (MODE == kGemmSwiGlu) {
         int sub = rr >> 4;
         seg = sub & 1;
-        row = tile_n * 64 + (sub >> 1) * 16 + (rr & 15);
-        col_base = tile_n * 64;
+        row = tile_n * (BN / 2) + (sub >> 1) * 16 + (rr & 15);
     } else {
         int n0 = tile_n * BN;
         int s = 0, start = 0;
@@ -70,224 +79,300 @@ __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, i
         }
         seg = s;
         row = n0 - start + rr;
-        col_base = n0;
     }
 }
 
+// Loads are unconditional with clamped addresses: a row past the weight's end
+// or a block past K only feeds outputs that are never stored, and keeping the
+// loop free of divergent loads lets the compiler count outstanding loads
+// exactly instead of draining the queue every stage.
 template <int TYPE>
-__device__ __forceinline__ void load_b(const QWeight &w, int row, int kb, int h, BRaw<TYPE> &b)
+__device__ __forceinline__ void load_chunk(const QWeight &w, int row, int kblk, int half, int nblk, BChunk &c)
 {
-    b.valid = row < w.rows;
-    if (!b.valid) return;
-    int nb = w.cols >> 5;
-    size_t blk = (size_t)row * nb + kb;
-    if (TYPE == kQ8_0) {
-        b.q = *(const u32x4 *)(w.qs + (size_t)row * w.cols + (size_t)kb * 32 + 16 * h);
-    } else {
-        b.q = *(const u32x4 *)(w.qs + (size_t)row * (w.cols >> 1) + (size_t)kb * 16);
-    }
-    b.d = h2f(w.d[blk]);
+    row = min(row, w.rows - 1);
+    kblk = min(kblk, nblk - 1);
+    size_t bi = (size_t)row * nblk + kblk;
+    if (TYPE == kQ8_0) c.q = *(const u32x4 *)(w.qs + (size_t)row * w.cols + (size_t)kblk * 32 + 16 * half);
+    else c.q = *(const u32x4 *)(w.qs + (size_t)row * (w.cols >> 1) + (size_t)kblk * 16);
+    c.d = w.d[bi];
     if (TYPE == kQ5_1) {
-        b.m = h2f(w.m[blk]);
-        b.qh = w.qh[blk] >> (16 * h);
+        c.m = w.m[bi];
+        c.qh = w.qh[bi];
     }
+    c.valid = true;
 }
 
-// The 16 quants of this thread's half block as fp16 integers, into LDS.
+// Decoded quants of one chunk as fp16 integers into the LDS row.
 template <int TYPE>
-__device__ __forceinline__ void store_b(const BRaw<TYPE> &b, int h, uint16_t *dst)
+__device__ __forceinline__ void store_chunk(const BChunk &c, int half, uint16_t *dst)
 {
-    uint32_t out[8];
-    if (!b.valid) {
+    u32x4 *d4 = (u32x4 *)dst;
+    if (!c.valid) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) out[i] = 0;
-    } else {
-        uint32_t wds[4] = {b.q.x, b.q.y, b.q.z, b.q.w};
+        for (int i = 0; i < Geo<TYPE>::EL / 8; i++) d4[i] = u32x4{0, 0, 0, 0};
+        return;
+    }
+    uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
+    if (TYPE == kQ8_0) {
+        uint32_t o[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            // elements 2i and 2i+1 of this half block
-            int e0 = 2 * i, e1 = 2 * i + 1;
-            float v0, v1;
-            if (TYPE == kQ8_0) {
-                v0 = (float)(int8_t)(wds[e0 >> 2] >> (8 * (e0 & 3)));
-                v1 = (float)(int8_t)(wds[e1 >> 2] >> (8 * (e1 & 3)));
-            } else {
-                uint32_t b0 = (wds[e0 >> 2] >> (8 * (e0 & 3))) & 0xff;
-                uint32_t b1 = (wds[e1 >> 2] >> (8 * (e1 & 3))) & 0xff;
-                int n0 = h ? (int)(b0 >> 4) : (int)(b0 & 15);
-                int n1 = h ? (int)(b1 >> 4) : (int)(b1 & 15);
-                if (TYPE == kQ4_0) {
-                    v0 = (float)(n0 - 8);
-                    v1 = (float)(n1 - 8);
-                } else {
-                    v0 = (float)(n0 | (int)(((b.qh >> e0) & 1u) << 4));
-                    v1 = (float)(n1 | (int)(((b.qh >> e1) & 1u) << 4));
-                }
-            }
-            out[i] = pack2(v0, v1);
+            uint32_t w0 = wd[i >> 1] >> (16 * (i & 1));
+            o[i] = pack2((float)(int8_t)(w0 & 0xff), (float)(int8_t)((w0 >> 8) & 0xff));
         }
+        d4[0] = u32x4{o[0], o[1], o[2], o[3]};
+        d4[1] = u32x4{o[4], o[5], o[6], o[7]};
+    } else {
+        // 32 elements: j < 16 low nibble of byte j, 16 + j high nibble.
+        uint32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            int e0 = 2 * i, e1 = 2 * i + 1;
+            int b0 = e0 & 15, b1 = e1 & 15;
+            uint32_t by0 = (wd[b0 >> 2] >> (8 * (b0 & 3))) & 0xff;
+            uint32_t by1 = (wd[b1 >> 2] >> (8 * (b1 & 3))) & 0xff;
+            int n0 = e0 < 16 ? (int)(by0 & 15) : (int)(by0 >> 4);
+            int n1 = e1 < 16 ? (int)(by1 & 15) : (int)(by1 >> 4);
+            float v0, v1;
+            if (TYPE == kQ4_0) {
+                v0 = (float)(n0 - 8);
+                v1 = (float)(n1 - 8);
+            } else {
+                v0 = (float)(n0 | (int)(((c.qh >> e0) & 1u) << 4));
+                v1 = (float)(n1 | (int)(((c.qh >> e1) & 1u) << 4));
+            }
+            o[i] = pack2(v0, v1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) d4[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
     }
-    u32x4 *d4 = (u32x4 *)dst;
-    d4[0] = u32x4{out[0], out[1], out[2], out[3]};
-    d4[1] = u32x4{out[4], out[5], out[6], out[7]};
+    (void)half;
 }
+
+// A fragments of one stage: [mi][kb2] hi and lo.
+template <int TM>
+struct AFrag {
+    half8_t hi[TM][2], lo[TM][2];
+    floatx4 s[TM][2]; // Q5_1 block sums of the lane's 4 C rows
+};
 
 } // namespace
 
-template <int TYPE, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a)
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int nt, int gm)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t As_hi[2][BM * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) uint16_t As_lo[2][BM * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_ROW];
-    __shared__ float Ds[2][BN];
-    __shared__ float Msh[2][TYPE == kQ5_1 ? BN : 1];
-    __shared__ __attribute__((aligned(16))) float Ss[2][TYPE == kQ5_1 ? BM : 4];
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    constexpr int CH = Geo<TYPE>::CH;
+    constexpr int CHUNKS = BN * CH;
+    constexpr int CPT = (CHUNKS + 255) / 256;
+    constexpr int NG = TN < 4 ? TN : 4; // N tiles per partial group
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LROW];
+    __shared__ float Ds[2][BN * 2];
+    __shared__ float Ms[2][TYPE == kQ5_1 ? BN * 2 : 1];
+
+    // ---- tile of this workgroup: contiguous per-XCD runs of a grouped order
+    const int total = gridDim.x;
+    const int per_xcd = total >> 3;
+    const int L = blockIdx.x;
+    const int Lp = (L & 7) * per_xcd + (L >> 3);
+    const int group = gm * nt;
+    const int first_m = (Lp / group) * gm;
+    const int gsz = min(mt - first_m, gm);
+    if (gsz <= 0) return;
+    const int tile_m = first_m + (Lp % group) % gsz;
+    const int tile_n = (Lp % group) / gsz;
+    if (tile_m >= mt || tile_n >= nt) return;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int tile_n = blockIdx.x, tile_m = blockIdx.y, z = blockIdx.z;
-    const int m0 = tile_m * BM;
+    const int wm = wave / WN, wn = wave % WN;
     const int M = a.M, K = a.K, nblk = K >> 5;
-    const int per = (nblk + a.ksplit - 1) / a.ksplit;
-    const int kb0 = z * per;
-    const int kb1 = min(nblk, kb0 + per);
+    const int nstage = (nblk + 1) >> 1;
+    const int m0 = tile_m * BM;
 
-    // Loader role: LDS row rr, half block h.
-    const int rr = tid >> 1, h = tid & 1;
-    int seg, wrow, col_base;
-    map_row<MODE>(a, tile_n, rr, seg, wrow, col_base);
-    const QWeight &w = a.seg[seg];
-    const int am = m0 + rr;
-    const bool a_ok = am < M;
-
-    u32x4 ahi[2], alo[2];
-    BRaw<TYPE> braw;
-    float s_next = 0.f;
-
-    auto load = [&](int kb) {
-        if (a_ok) {
-            const u32x4 *ph = (const u32x4 *)(a.xhi + (size_t)am * K + (size_t)kb * 32 + 16 * h);
-            const u32x4 *pl = (const u32x4 *)(a.xlo + (size_t)am * K + (size_t)kb * 32 + 16 * h);
-            ahi[0] = ph[0];
-            ahi[1] = ph[1];
-            alo[0] = pl[0];
-            alo[1] = pl[1];
-            if (TYPE == kQ5_1) s_next = a.xsum[(size_t)am * nblk + kb];
-        } else {
-            ahi[0] = ahi[1] = alo[0] = alo[1] = u32x4{0, 0, 0, 0};
-            s_next = 0.f;
+    // ---- loader role (B): chunk ids tid + 256 j
+    int c_row[CPT], c_ch[CPT], c_seg[CPT], c_wrow[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        int c = tid + 256 * j;
+        c_row[j] = c < CHUNKS ? c / CH : -1; // -1: no chunk (loads a duplicate, stores nothing)
+        c_ch[j] = c % CH;
+        map_row<MODE, BN>(a, tile_n, c < CHUNKS ? c / CH : 0, c_seg[j], c_wrow[j]);
+    }
+    auto load_b = [&](int st, BChunk (&br)[CPT]) {
+        st = min(st, nstage - 1);
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            int kblk, half;
+            if (TYPE == kQ8_0) {
+                kblk = 2 * st + (c_ch[j] >> 1);
+                half = c_ch[j] & 1;
+            } else {
+                kblk = 2 * st + c_ch[j];
+                half = 0;
+            }
+            load_chunk<TYPE>(a.seg[c_seg[j]], c_wrow[j], kblk, half, nblk, br[j]);
         }
-        load_b<TYPE>(w, wrow, kb, h, braw);
     };
-    auto store = [&](int st) {
-        u32x4 *dh = (u32x4 *)(&As_hi[st][rr * LDS_ROW + 16 * h]);
-        u32x4 *dl = (u32x4 *)(&As_lo[st][rr * LDS_ROW + 16 * h]);
-        dh[0] = ahi[0];
-        dh[1] = ahi[1];
-        dl[0] = alo[0];
-        dl[1] = alo[1];
-        store_b<TYPE>(braw, h, &Bs[st][rr * LDS_ROW + 16 * h]);
-        if (h == 0) {
-            Ds[st][rr] = braw.valid ? braw.d : 0.f;
-            if (TYPE == kQ5_1) {
-                Msh[st][rr] = braw.valid ? braw.m : 0.f;
-                Ss[st][rr] = s_next;
+    auto store_b = [&](int buf, const BChunk (&br)[CPT]) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            if (c_row[j] < 0) continue;
+            int rr = c_row[j];
+            int kb2 = TYPE == kQ8_0 ? (c_ch[j] >> 1) : c_ch[j];
+            int half = TYPE == kQ8_0 ? (c_ch[j] & 1) : 0;
+            store_chunk<TYPE>(br[j], half, &Bs[buf][rr * LROW + kb2 * 32 + half * 16]);
+            if (half == 0) {
+                Ds[buf][rr * 2 + kb2] = br[j].valid ? h2f(br[j].d) : 0.f;
+                if (TYPE == kQ5_1) Ms[buf][rr * 2 + kb2] = br[j].valid ? h2f(br[j].m) : 0.f;
             }
         }
     };
 
-    floatx4 acc[4][4];
+    // ---- A fragments straight from global memory: each is one contiguous
+    // 1 KiB operand tile (xt_index layout), one 16-byte load per lane.
+    const int rg0 = (m0 >> 4) + wm * TM;
+    const int frag_k = 8 * (lane >> 4); // k offset of this lane's B fragment within a block
+    const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
+    auto load_a = [&](int st, AFrag<TM> &f) {
+        st = min(st, nstage - 1);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int mi = 0; mi < TM; mi++) {
+            int rg = min(rg0 + mi, rg_last);
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int kb2 = 0; kb2 < 2; kb2++) {
+                int kblk = min(2 * st + kb2, nblk - 1);
+                const uint16_t *tile = a.xt + (((size_t)rg * nblk + kblk) * 2) * 512 + lane * 8;
+                f.hi[mi][kb2] = *(const half8_t *)tile;
+                f.lo[mi][kb2] = *(const half8_t *)(tile + 512);
+                if (TYPE == kQ5_1) {
+                    int crow = m0 + wm * TM * 16 + mi * 16 + 4 * (lane >> 4);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) f.s[mi][kb2][r] = a.xsum[(size_t)min(crow + r, M - 1) * nblk + kblk];
+                }
+            }
+        }
+    };
 
-    if (kb0 < kb1) {
-        load(kb0);
-        store(0);
-    }
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Per block: p = x_hi . q, p += x_lo . q (MFMA), acc = fma(d, p, acc)
+    // (+ m * sum(x)).  KS blocks' partials are in flight together so each MFMA
+    // result is consumed several MFMAs after it issues; the FMAs still apply
+    // block 0 before block 1 for every output.
+    constexpr int KS = TM * NG >= 8 ? 1 : 2;
+    auto compute = [&](int st, int buf, const AFrag<TM> &f) {
+        const bool second = 2 * st + 1 < nblk;
+#pragma unroll
+        for (int k0 = 0; k0 < 2; k0 += KS) {
+#pragma unroll
+            for (int g = 0; g < TN / NG; g++) {
+                half8_t fb[KS][NG];
+                float dsc[KS][NG], mn[KS][NG];
+                floatx4 p[KS][TM][NG];
+#pragma unroll
+                for (int kk = 0; kk < KS; kk++)
+#pragma unroll
+                    for (int n = 0; n < NG; n++) {
+                        int c = wn * TN * 16 + (g * NG + n) * 16 + (lane & 15);
+                        fb[kk][n] = *(const half8_t *)(&Bs[buf][c * LROW + (k0 + kk) * 32 + frag_k]);
+                        dsc[kk][n] = Ds[buf][c * 2 + k0 + kk];
+                        if (TYPE == kQ5_1) mn[kk][n] = Ms[buf][c * 2 + k0 + kk];
+                    }
+#pragma unroll
+                for (int kk = 0; kk < KS; kk++)
+#pragma unroll
+                    for (int mi = 0; mi < TM; mi++)
+#pragma unroll
+                        for (int n = 0; n < NG; n++)
+                            p[kk][mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.hi[mi][k0 + kk], fb[kk][n],
+                                                                                   floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int kk = 0; kk < KS; kk++)
+#pragma unroll
+                    for (int mi = 0; mi < TM; mi++)
+#pragma unroll
+                        for (int n = 0; n < NG; n++)
+                            p[kk][mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.lo[mi][k0 + kk], fb[kk][n],
+                                                                                   p[kk][mi][n], 0, 0, 0);
+#pragma unroll
+                for (int kk = 0; kk < KS; kk++) {
+                    if (k0 + kk == 1 && !second) break; // odd block count: no second block
+#pragma unroll
+                    for (int mi = 0; mi < TM; mi++)
+#pragma unroll
+                        for (int n = 0; n < NG; n++)
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                float v = fmaf(dsc[kk][n], p[kk][mi][n][r], acc[mi][g * NG + n][r]);
+                                if (TYPE == kQ5_1) v = fmaf(mn[kk][n], f.s[mi][k0 + kk][r], v);
+                                acc[mi][g * NG + n][r] = v;
+                            }
+                }
+            }
+        }
+    };
+
+    // ---- prologue: stage 0 decoded into LDS, stages 1 and 2 raw in registers
+    BChunk br0[CPT], br1[CPT];
+    AFrag<TM> fa0, fa1;
+    load_b(0, br0);
+    load_b(1, br1);
+    load_a(0, fa0);
+    store_b(0, br0);
+    load_b(2, br0);
     __syncthreads();
 
-    const int frag_row = lane & 15, frag_k = 8 * (lane >> 4);
-    for (int kb = kb0; kb < kb1; kb++) {
-        const int st = (kb - kb0) & 1;
-        if (kb + 1 < kb1) load(kb + 1);
-
-        half8_t fa_hi[4], fa_lo[4], fb[4];
-        float dsc[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            int r = 64 * wm + 16 * i + frag_row;
-            fa_hi[i] = *(const half8_t *)(&As_hi[st][r * LDS_ROW + frag_k]);
-            fa_lo[i] = *(const half8_t *)(&As_lo[st][r * LDS_ROW + frag_k]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            int c = 64 * wn + 16 * j + frag_row;
-            fb[j] = *(const half8_t *)(&Bs[st][c * LDS_ROW + frag_k]);
-            dsc[j] = Ds[st][c];
-        }
-        floatx4 p[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                p[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa_hi[i], fb[j], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) p[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa_lo[i], fb[j], p[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(dsc[j], p[i][j][r], acc[i][j][r]);
-        if (TYPE == kQ5_1) {
-            float mn[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) mn[j] = Msh[st][64 * wn + 16 * j + frag_row];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                floatx4 sv = *(const floatx4 *)(&Ss[st][64 * wm + 16 * i + 4 * (lane >> 4)]);
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] = fmaf(mn[j], sv[r], acc[i][j][r]);
-            }
-        }
-        if (kb + 1 < kb1) store(st ^ 1);
+    // Iteration s: compute on stage s (LDS buffer s & 1, A regs), decode stage
+    // s + 1 from its raw registers, refill those registers with stage s + 3.
+    int s = 0;
+    for (; s + 1 < nstage; s += 2) {
+        load_a(s + 1, fa1);
+        compute(s, 0, fa0);
+        store_b(1, br1);
+        load_b(s + 3, br1);
+        __syncthreads();
+        load_a(s + 2, fa0);
+        compute(s + 1, 1, fa1);
+        store_b(0, br0);
+        load_b(s + 4, br0);
         __syncthreads();
     }
+    if (s < nstage) compute(s, 0, fa0);
 
-    // Epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
-    const int row_base = m0 + 64 * wm + 4 * (lane >> 4);
+    // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
+    const int row_base = m0 + wm * TM * 16 + 4 * (lane >> 4);
     if (MODE == kGemmStore) {
-        float *y = a.y + (size_t)z * M * a.ldy;
-        const QWeight &ws = a.seg[seg]; // segment of this workgroup's columns
-        int seg_start = col_base;       // global column of the tile's first row
+        float *y = a.y;
+        int seg, r0;
+        map_row<MODE, BN>(a, tile_n, 0, seg, r0); // segment and local row of the tile's first column
+        const QWeight &ws = a.seg[seg];
+        const int col0 = tile_n * BN;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int j = 0; j < TN; j++) {
+            int off = wn * TN * 16 + j * 16 + (lane & 15);
+            if (r0 + off >= ws.rows) continue;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                int col = seg_start + 64 * wn + 16 * j + frag_row;
-                int local = wrow - rr + 64 * wn + 16 * j + frag_row; // row within the segment
-                if (local >= ws.rows) continue;
+            for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     int row = row_base + 16 * i + r;
-                    if (row < M) y[(size_t)row * a.ldy + col] = acc[i][j][r];
+                    if (row < M) y[(size_t)row * a.ldy + col0 + off] = acc[i][j][r];
                 }
-            }
+        }
     } else {
         const int ld = a.seg[0].rows;
+        const int cbase = tile_n * (BN / 2);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int pp = 0; pp < TN / 2; pp++) {
+            // N tiles 2pp (gate) and 2pp+1 (up) of this wave cover the same outputs
+            int col = cbase + ((wn * TN + 2 * pp) >> 1) * 16 + (lane & 15);
+            if (col >= ld) continue;
 #pragma unroll
-            for (int pp = 0; pp < 2; pp++) {
-                int col = col_base + (2 * wn + pp) * 16 + frag_row;
-                if (col >= ld) continue;
+            for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     int row = row_base + 16 * i + r;
@@ -300,39 +385,58 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a)
                     float v = sg * gu;
                     uint16_t hi, lo;
                     split_f16(v, hi, lo);
-                    a.ohi[(size_t)row * ld + col] = hi;
-                    a.olo[(size_t)row * ld + col] = lo;
+                    a.ot[xt_index(row, col, ld >> 5, 0)] = hi;
+                    a.ot[xt_index(row, col, ld >> 5, 1)] = lo;
                 }
-            }
+        }
     }
+}
+
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN>
+static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
+{
+    constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
+    int mt = (a.M + BM - 1) / BM;
+    int ncols;
+    if (MODE == kGemmSwiGlu) {
+        ncols = (a.seg[0].rows + BN / 2 - 1) / (BN / 2);
+    } else {
+        int ntot = 0;
+        for (int i = 0; i < a.nseg; i++) ntot += a.seg[i].rows;
+        ncols = (ntot + BN - 1) / BN;
+    }
+    int gm = mt <= 8 ? mt : 8;
+    int tiles = mt * ncols;
+    int grid = (tiles + 7) & ~7;
+    hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
+    return hipGetLastError();
+}
+
+template <int TYPE, int MODE>
+static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
+{
+    // Shape choice by M only changes which rows share a tile, never a result bit.
+    if (a.M <= 512) return launch_cfg<TYPE, MODE, 2, 2, 2, 2>(a, s);
+    return launch_cfg<TYPE, MODE, 4, 1, 2, 8>(a, s);
 }
 
 template <int TYPE>
 static hipError_t launch_typed(const GemmArgs &a, hipStream_t s)
 {
-    int mt = (a.M + BM - 1) / BM;
-    if (a.mode == kGemmSwiGlu) {
-        int nt = (a.seg[0].rows + 63) / 64;
-        hipLaunchKernelGGL((gemm_q_kernel<TYPE, kGemmSwiGlu>), dim3(nt, mt, 1), dim3(256), 0, s, a);
-    } else {
-        int ntot = 0;
-        for (int i = 0; i < a.nseg; i++) ntot += a.seg[i].rows;
-        int nt = (ntot + BN - 1) / BN;
-        hipLaunchKernelGGL((gemm_q_kernel<TYPE, kGemmStore>), dim3(nt, mt, a.ksplit), dim3(256), 0, s, a);
-    }
-    return hipGetLastError();
+    if (a.mode == kGemmSwiGlu) return launch_mode<TYPE, kGemmSwiGlu>(a, s);
+    return launch_mode<TYPE, kGemmStore>(a, s);
 }
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s)
 {
     if (a.M <= 0) return hipSuccess;
-    if (a.K % 32 != 0 || a.ksplit < 1) return hipErrorInvalidValue;
+    if (a.K % 32 != 0 || a.ksplit != 1) return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; i++) {
         if (a.seg[i].type != a.seg[0].type || a.seg[i].cols != a.K) return hipErrorInvalidValue;
-        // every segment but the last must tile exactly into 128-row tiles
-        if (a.mode == kGemmStore && i + 1 < a.nseg && a.seg[i].rows % BN != 0) return hipErrorInvalidValue;
+        // every segment but the last must tile exactly (both tile widths divide 64)
+        if (a.mode == kGemmStore && i + 1 < a.nseg && a.seg[i].rows % 128 != 0) return hipErrorInvalidValue;
     }
-    if (a.mode == kGemmSwiGlu && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows || a.ksplit != 1))
+    if (a.mode == kGemmSwiGlu && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows || a.seg[0].rows % 32 != 0))
         return hipErrorInvalidValue;
     switch (a.seg[0].type) {
     case kQ8_0: return launch_typed<kQ8_0>(a, s);

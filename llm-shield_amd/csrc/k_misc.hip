@@ -68,33 +68,47 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
     __syncthreads();
     double sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
     float scale = 1.0f / sqrtf((float)(sum / a.D) + a.eps);
-    for (int i = threadIdx.x; i < a.D; i += 256) {
-        float x = add && !a.store_h ? h[i] + add[i] : h[i];
-        float v = x * scale;
-        float y = v * a.w[i];
-        size_t o = (size_t)t * a.D + i;
-        if (a.out32) a.out32[o] = y;
-        if (a.ohi) {
-            uint16_t hi, lo;
-            split_f16(y, hi, lo);
-            a.ohi[o] = hi;
-            a.olo[o] = lo;
+    const int nblk = a.D >> 5;
+    if (a.out32) {
+        for (int i = threadIdx.x; i < a.D; i += 256) {
+            float x = add && !a.store_h ? h[i] + add[i] : h[i];
+            float v = x * scale;
+            a.out32[(size_t)t * a.D + i] = v * a.w[i];
         }
     }
-    if (a.xsum) {
-        // Per-32 block sums of the (hi + lo) values the GEMM will see, staged
-        // through LDS (the host only asks for them when D <= kNormSumMax).
+    if (a.ot) {
+        // eight consecutive k per thread: one 16-byte store per part
         __shared__ float stage[kNormSumMax];
-        for (int i = threadIdx.x; i < a.D; i += 256) {
-            size_t o = (size_t)t * a.D + i;
-            stage[i] = h2f(a.ohi[o]) + h2f(a.olo[o]);
+        for (int g = threadIdx.x; g < (a.D >> 3); g += 256) {
+            uint32_t hv[4], lv[4];
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                int i = 8 * g + j;
+                float x0 = add && !a.store_h ? h[i] + add[i] : h[i];
+                float x1 = add && !a.store_h ? h[i + 1] + add[i + 1] : h[i + 1];
+                float v0 = x0 * scale, v1 = x1 * scale;
+                float y0 = v0 * a.w[i], y1 = v1 * a.w[i + 1];
+                uint16_t h0, l0, h1, l1;
+                split_f16(y0, h0, l0);
+                split_f16(y1, h1, l1);
+                hv[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                lv[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                if (a.xsum) {
+                    stage[i] = h2f(h0) + h2f(l0);
+                    stage[i + 1] = h2f(h1) + h2f(l1);
+                }
+            }
+            *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 1)) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
         }
-        __syncthreads();
-        int nb = a.D >> 5;
-        for (int b = threadIdx.x; b < nb; b += 256) {
-            float s = 0.f;
-            for (int j = 0; j < 32; j++) s += stage[b * 32 + j];
-            a.xsum[(size_t)t * nb + b] = s;
+        if (a.xsum) {
+            // per-32 block sums of the (hi + lo) values the GEMM will see
+            __syncthreads();
+            for (int b = threadIdx.x; b < nblk; b += 256) {
+                float s = 0.f;
+                for (int j = 0; j < 32; j++) s += stage[b * 32 + j];
+                a.xsum[(size_t)t * nblk + b] = s;
+            }
         }
     }
 }
@@ -102,29 +116,30 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
 hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.xsum && (a.D > kNormSumMax || !a.ohi)) return hipErrorInvalidValue;
+    if (a.ot && (a.D > kNormSumMax || a.D % 32 != 0)) return hipErrorInvalidValue;
+    if (a.xsum && !a.ot) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
-__global__ void block_sums_kernel(const uint16_t *hi, const uint16_t *lo, int D, float *xsum)
+__global__ void block_sums_kernel(const uint16_t *xt, int D, float *xsum)
 {
     int t = blockIdx.x;
     int nb = D >> 5;
     for (int b = threadIdx.x; b < nb; b += blockDim.x) {
         float s = 0.f;
         for (int j = 0; j < 32; j++) {
-            size_t o = (size_t)t * D + b * 32 + j;
-            s += h2f(hi[o]) + h2f(lo[o]);
+            int k = b * 32 + j;
+            s += h2f(xt[xt_index(t, k, nb, 0)]) + h2f(xt[xt_index(t, k, nb, 1)]);
         }
         xsum[(size_t)t * nb + b] = s;
     }
 }
 
-hipError_t launch_block_sums(const uint16_t *hi, const uint16_t *lo, int T, int D, float *xsum, hipStream_t s)
+hipError_t launch_block_sums(const uint16_t *xt, int T, int D, float *xsum, hipStream_t s)
 {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(block_sums_kernel, dim3(T), dim3(128), 0, s, hi, lo, D, xsum);
+    hipLaunchKernelGGL(block_sums_kernel, dim3(T), dim3(128), 0, s, xt, D, xsum);
     return hipGetLastError();
 }
 
@@ -283,20 +298,23 @@ hipError_t launch_argmax(const float *x, int n, int32_t *result, float *sv, int3
 
 // ------------------------------------------------------------ fp32 -> fp16 pair
 
-__global__ void split_kernel(const float *x, size_t n, uint16_t *hi, uint16_t *lo)
+__global__ void split_kernel(const float *x, int T, int D, uint16_t *xt)
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+    if (i >= (size_t)T * D) return;
+    int t = (int)(i / D), k = (int)(i % D);
     uint16_t a, b;
     split_f16(x[i], a, b);
-    hi[i] = a;
-    lo[i] = b;
+    xt[xt_index(t, k, D >> 5, 0)] = a;
+    xt[xt_index(t, k, D >> 5, 1)] = b;
 }
 
-hipError_t launch_split(const float *x, size_t n, uint16_t *hi, uint16_t *lo, hipStream_t s)
+hipError_t launch_split(const float *x, int T, int D, uint16_t *xt, hipStream_t s)
 {
+    size_t n = (size_t)T * D;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, hi, lo);
+    if (D % 32 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, T, D, xt);
     return hipGetLastError();
 }
 

@@ -113,7 +113,7 @@ struct jev_ctx {
 
     // workspace
     DevBuf<float> h, y, yo, ydown, q, x32, ctx32, f32, xn, logits, part, xsum;
-    DevBuf<uint16_t> xhi, xlo, fhi, flo;
+    DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
     DevBuf<int32_t> ints;
     DevBuf<AttnTile> tiles;
     DevBuf<float> amax_v;
@@ -309,8 +309,8 @@ bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a
 
 // One linear step y = x . W^T over up to three weights sharing x.  T >= 2:
 // MFMA GEMM on the fp16 pair; T == 1: GEMV on fp32 x.
-int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xhi, const uint16_t *xlo,
-           const float *xsum, const float *x32, float *y, int ldy)
+int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xt, const float *xsum,
+           const float *x32, float *y, int ldy)
 {
     double nrows = 0, wbytes = 0;
     for (int i = 0; i < nw; i++) {
@@ -333,8 +333,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     GemmArgs g;
     g.M = T;
     g.K = ws[0]->cols;
-    g.xhi = xhi;
-    g.xlo = xlo;
+    g.xt = xt;
     g.xsum = xsum;
     g.nseg = nw;
     for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
@@ -361,19 +360,15 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
         HIP_TRY(c->f32.ensure((size_t)f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
     } else {
-        HIP_TRY(c->xhi.ensure((size_t)T * std::max(f.hidden, c->qdim())));
-        HIP_TRY(c->xlo.ensure((size_t)T * std::max(f.hidden, c->qdim())));
-        HIP_TRY(c->fhi.ensure((size_t)T * f.ffn));
-        HIP_TRY(c->flo.ensure((size_t)T * f.ffn));
+        size_t T16 = ((size_t)T + 15) & ~(size_t)15;
+        HIP_TRY(c->xt.ensure(T16 * std::max(f.hidden, c->qdim()) * 2));
+        HIP_TRY(c->ft.ensure(T16 * f.ffn * 2));
     }
     size_t nx = std::max(1, n_out);
     HIP_TRY(c->xn.ensure(nx * f.hidden));
     if (mode == JEV_OUT_FULL || mode == JEV_OUT_LAST_FULL) {
         HIP_TRY(c->logits.ensure(nx * (size_t)f.vocab));
-        if (nx >= 2) {
-            HIP_TRY(c->xhi.ensure(std::max(c->xhi.n, nx * f.hidden)));
-            HIP_TRY(c->xlo.ensure(std::max(c->xlo.n, nx * f.hidden)));
-        }
+        if (nx >= 2) HIP_TRY(c->xt.ensure(std::max(c->xt.n, ((nx + 15) & ~(size_t)15) * f.hidden * 2)));
     }
     HIP_TRY(c->amax_v.ensure(512));
     HIP_TRY(c->amax_i.ensure(512));
@@ -553,8 +548,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         na.eps = f.rms_eps;
         if (T == 1) na.out32 = c->x32.p;
         else {
-            na.ohi = c->xhi.p;
-            na.olo = c->xlo.p;
+            na.ot = c->xt.p;
             if (L.q.type == kQ5_1) na.xsum = c->xsum.p;
         }
         HIP_TRY(launch_rmsnorm(na, s));
@@ -564,14 +558,14 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         bool fuse = same_type3(L.q, L.k, L.v) && (T == 1 || (qdim % 128 == 0 && kvdim % 128 == 0));
         if (fuse) {
             const QWeight *ws[3] = {&L.q, &L.k, &L.v};
-            int rc = linear(c, T, ws, 3, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, c->y.p, ldqkv);
+            int rc = linear(c, T, ws, 3, c->xt.p, c->xsum.p, c->x32.p, c->y.p, ldqkv);
             if (rc) return rc;
         } else {
             const QWeight *wq[1] = {&L.q}, *wk[1] = {&L.k}, *wv[1] = {&L.v};
             float *yq = c->y.p, *yk = c->y.p + qdim, *yv = c->y.p + qdim + kvdim;
-            int rc = linear(c, T, wq, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yq, ldqkv);
-            if (!rc) rc = linear(c, T, wk, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yk, ldqkv);
-            if (!rc) rc = linear(c, T, wv, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->x32.p, yv, ldqkv);
+            int rc = linear(c, T, wq, 1, c->xt.p, c->xsum.p, c->x32.p, yq, ldqkv);
+            if (!rc) rc = linear(c, T, wk, 1, c->xt.p, c->xsum.p, c->x32.p, yk, ldqkv);
+            if (!rc) rc = linear(c, T, wv, 1, c->xt.p, c->xsum.p, c->x32.p, yv, ldqkv);
             if (rc) return rc;
         }
         if (T == 1 && !fuse) {
@@ -636,18 +630,17 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             aa.vc = vc;
             aa.cap = c->cap;
             aa.scale = scale;
-            aa.ohi = c->xhi.p;
-            aa.olo = c->xlo.p;
+            aa.ot = c->xt.p;
             {
                 ProfScope ps(c, JEV_PROF_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                              8.0 * f.head_dim * f.n_kv_heads * p.kv_rows + 8.0 * T * qdim);
                 HIP_TRY(launch_attn_tree(aa, s));
             }
-            if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xhi.p, c->xlo.p, T, qdim, c->xsum.p, s));
+            if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xt.p, T, qdim, c->xsum.p, s));
         }
         {
             const QWeight *wo[1] = {&L.o};
-            int rc = linear(c, T, wo, 1, c->xhi.p, c->xlo.p, c->xsum.p, c->ctx32.p, c->yo.p, D);
+            int rc = linear(c, T, wo, 1, c->xt.p, c->xsum.p, c->ctx32.p, c->yo.p, D);
             if (rc) return rc;
         }
 
@@ -673,23 +666,21 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             GemmArgs g;
             g.M = T;
             g.K = D;
-            g.xhi = c->xhi.p;
-            g.xlo = c->xlo.p;
+            g.xt = c->xt.p;
             g.xsum = c->xsum.p;
             g.nseg = 2;
             g.seg[0] = L.gate;
             g.seg[1] = L.up;
             g.mode = kGemmSwiGlu;
-            g.ohi = c->fhi.p;
-            g.olo = c->flo.p;
+            g.ot = c->ft.p;
             ProfScope ps(c, JEV_PROF_GEMM, 4.0 * T * f.ffn * D,
                          weight_bytes(L.gate) + weight_bytes(L.up) + T * (4.0 * D + 4.0 * f.ffn));
             HIP_TRY(launch_gemm(g, s));
-            if (L.down.type == kQ5_1) HIP_TRY(launch_block_sums(c->fhi.p, c->flo.p, T, f.ffn, c->xsum.p, s));
+            if (L.down.type == kQ5_1) HIP_TRY(launch_block_sums(c->ft.p, T, f.ffn, c->xsum.p, s));
         }
         {
             const QWeight *wd[1] = {&L.down};
-            int rc = linear(c, T, wd, 1, c->fhi.p, c->flo.p, c->xsum.p, c->f32.p, c->ydown.p, D);
+            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D);
             if (rc) return rc;
         }
     }
@@ -734,15 +725,13 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows));
         HIP_TRY(launch_gemv(g, s));
     } else {
-        fn.ohi = c->xhi.p;
-        fn.olo = c->xlo.p;
+        fn.ot = c->xt.p;
         fn.xsum = tab.type == kQ5_1 ? c->xsum.p : nullptr;
         HIP_TRY(launch_rmsnorm(fn, s));
         GemmArgs g;
         g.M = p.n_out;
         g.K = D;
-        g.xhi = c->xhi.p;
-        g.xlo = c->xlo.p;
+        g.xt = c->xt.p;
         g.xsum = c->xsum.p;
         g.nseg = 1;
         g.seg[0] = tab;
@@ -882,8 +871,7 @@ void jev_destroy(jev_ctx *c)
     if (c->vc) (void)hipFree(c->vc);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
-    c->part.release(); c->xsum.release(); c->xhi.release(); c->xlo.release(); c->fhi.release();
-    c->flo.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
     if (c->copied) (void)hipEventDestroy(c->copied);
@@ -1261,22 +1249,21 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
     if (rc) return rc;
     size_t nx = (size_t)tokens * cols, ny = (size_t)tokens * rows;
     float *dx = nullptr, *dy = nullptr, *dsum = nullptr;
-    uint16_t *hi = nullptr, *lo = nullptr;
+    uint16_t *xt = nullptr;
     hipError_t e = hipMalloc((void **)&dx, nx * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess && tokens >= 2) {
-        e = hipMalloc((void **)&hi, nx * 2);
-        if (e == hipSuccess) e = hipMalloc((void **)&lo, nx * 2);
+        size_t t16 = ((size_t)tokens + 15) & ~(size_t)15;
+        e = hipMalloc((void **)&xt, t16 * cols * 2 * sizeof(uint16_t));
         if (e == hipSuccess) e = hipMalloc((void **)&dsum, (nx / 32 + 1) * sizeof(float));
-        if (e == hipSuccess) e = launch_split(dx, nx, hi, lo, nullptr);
-        if (e == hipSuccess && type == kQ5_1) e = launch_block_sums(hi, lo, tokens, (int)cols, dsum, nullptr);
+        if (e == hipSuccess) e = launch_split(dx, tokens, (int)cols, xt, nullptr);
+        if (e == hipSuccess && type == kQ5_1) e = launch_block_sums(xt, tokens, (int)cols, dsum, nullptr);
         if (e == hipSuccess) {
             GemmArgs g;
             g.M = tokens;
             g.K = (int)cols;
-            g.xhi = hi;
-            g.xlo = lo;
+            g.xt = xt;
             g.xsum = dsum;
             g.seg[0] = w;
             g.ldy = (int)rows;
@@ -1292,7 +1279,7 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
         e = launch_gemv(g, nullptr);
     }
     if (e == hipSuccess) e = hipMemcpy(y, dy, ny * sizeof(float), hipMemcpyDeviceToHost);
-    for (void *pp : {(void *)dx, (void *)dy, (void *)dsum, (void *)hi, (void *)lo})
+    for (void *pp : {(void *)dx, (void *)dy, (void *)dsum, (void *)xt})
         if (pp) (void)hipFree(pp);
     free_weight(w);
     if (e != hipSuccess) return fail(JEV_EDEVICE, "matmul: %s", hipGetErrorString(e));

@@ -59,7 +59,7 @@ def test_gpu_dequant_random_blocks_bit_exact(gpu, t):
 
 
 SHAPES = [(128, 256, 1), (64, 3072, 5), (128, 3072, 13), (64, 4096, 6), (64, 9216, 7), (256, 512, 2),
-          (384, 1024, 130), (3072, 3072, 256), (1024, 3072, 1)]
+          (384, 1024, 130), (3072, 3072, 256), (1024, 3072, 1), (384, 1088, 700), (200, 512, 513)]
 
 
 @pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
@@ -77,13 +77,16 @@ def test_gpu_matmul_matches_oracle(gpu, t, rows, cols, tokens):
 def test_gpu_matmul_batch_invariance_bitwise(gpu, t):
     # A token's result does not depend on its batch (PanelGemmTests.cs:61-74),
     # across the M tile boundary (128) too.
+    # Small-M and large-M calls take different tile shapes; bits must not move.
     rows, cols = 384, 3072
     raw = jev.synth_tensor("inv", t, rows, cols)
-    x = np.random.default_rng(1).standard_normal((300, cols)).astype(np.float32)
-    full = matmul_gpu(t, raw, rows, cols, x, 300)
+    x = np.random.default_rng(1).standard_normal((700, cols)).astype(np.float32)
+    full = matmul_gpu(t, raw, rows, cols, x, 700)
+    mid = matmul_gpu(t, raw, rows, cols, x[:300], 300)
     part = matmul_gpu(t, raw, rows, cols, x[120:137], 17)
+    assert np.array_equal(full[:300], mid)
     assert np.array_equal(full[120:137], part)
-    again = matmul_gpu(t, raw, rows, cols, x, 300)
+    again = matmul_gpu(t, raw, rows, cols, x, 700)
     assert np.array_equal(full, again)
 
 
