@@ -45,8 +45,6 @@ struct alignas(16) u32x4 {
     uint32_t x, y, z, w;
 };
 
-__device__ __forceinline__ uint16_t h16(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return (uint32_t)h16(a) | ((uint32_t)h16(b) << 16); }
 
 // One loader chunk: 16 bytes of quants (Q8_0: 16 elements = half a block;
 // Q4_0/Q5_1: one whole block of 32) plus its block's scale fields.
@@ -86,20 +84,30 @@ __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, i
 // or a block past K only feeds outputs that are never stored, and keeping the
 // loop free of divergent loads lets the compiler count outstanding loads
 // exactly instead of draining the queue every stage.
-template <int TYPE>
-__device__ __forceinline__ void load_chunk(const QWeight &w, int row, int kblk, int half, int nblk, BChunk &c)
+
+// Integer quants to fp16 without float conversions: a byte u placed under
+// the exponent byte 0x64 is the fp16 value 1024 + u (exact, ulp 1 in
+// [1024, 2048)); one packed fp16 subtraction of the bias then leaves the
+// integer.  Four values cost one byte permute per pair plus one v_pk_add_f16
+// per pair.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t biased_pair(uint32_t bytes, uint32_t sel)
 {
-    row = min(row, w.rows - 1);
-    kblk = min(kblk, nblk - 1);
-    size_t bi = (size_t)row * nblk + kblk;
-    if (TYPE == kQ8_0) c.q = *(const u32x4 *)(w.qs + (size_t)row * w.cols + (size_t)kblk * 32 + 16 * half);
-    else c.q = *(const u32x4 *)(w.qs + (size_t)row * (w.cols >> 1) + (size_t)kblk * 16);
-    c.d = w.d[bi];
-    if (TYPE == kQ5_1) {
-        c.m = w.m[bi];
-        c.qh = w.qh[bi];
-    }
-    c.valid = true;
+    return __builtin_amdgcn_perm(0x64646464u, bytes, sel);
+}
+
+__device__ __forceinline__ uint32_t sub_bias(uint32_t v, _Float16 bias)
+{
+    half2_t h = __builtin_bit_cast(half2_t, v) - half2_t{bias, bias};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four biased bytes -> two fp16 pairs (elements 0,1 and 2,3).
+__device__ __forceinline__ void bytes_to_f16(uint32_t bytes, _Float16 bias, uint32_t &p01, uint32_t &p23)
+{
+    p01 = sub_bias(biased_pair(bytes, 0x04010400u), bias);
+    p23 = sub_bias(biased_pair(bytes, 0x04030402u), bias);
 }
 
 // Decoded quants of one chunk as fp16 integers into the LDS row.
@@ -107,41 +115,29 @@ template <int TYPE>
 __device__ __forceinline__ void store_chunk(const BChunk &c, int half, uint16_t *dst)
 {
     u32x4 *d4 = (u32x4 *)dst;
-    if (!c.valid) {
-#pragma unroll
-        for (int i = 0; i < Geo<TYPE>::EL / 8; i++) d4[i] = u32x4{0, 0, 0, 0};
-        return;
-    }
     uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
     if (TYPE == kQ8_0) {
+        // int8 q: bias by 128 (flip the sign bit), then subtract 1152.
         uint32_t o[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            uint32_t w0 = wd[i >> 1] >> (16 * (i & 1));
-            o[i] = pack2((float)(int8_t)(w0 & 0xff), (float)(int8_t)((w0 >> 8) & 0xff));
-        }
+        for (int i = 0; i < 4; i++) bytes_to_f16(wd[i] ^ 0x80808080u, (_Float16)1152.0f, o[2 * i], o[2 * i + 1]);
         d4[0] = u32x4{o[0], o[1], o[2], o[3]};
         d4[1] = u32x4{o[4], o[5], o[6], o[7]};
     } else {
         // 32 elements: j < 16 low nibble of byte j, 16 + j high nibble.
+        const _Float16 bias = TYPE == kQ4_0 ? (_Float16)1032.0f : (_Float16)1024.0f;
         uint32_t o[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            int e0 = 2 * i, e1 = 2 * i + 1;
-            int b0 = e0 & 15, b1 = e1 & 15;
-            uint32_t by0 = (wd[b0 >> 2] >> (8 * (b0 & 3))) & 0xff;
-            uint32_t by1 = (wd[b1 >> 2] >> (8 * (b1 & 3))) & 0xff;
-            int n0 = e0 < 16 ? (int)(by0 & 15) : (int)(by0 >> 4);
-            int n1 = e1 < 16 ? (int)(by1 & 15) : (int)(by1 >> 4);
-            float v0, v1;
-            if (TYPE == kQ4_0) {
-                v0 = (float)(n0 - 8);
-                v1 = (float)(n1 - 8);
-            } else {
-                v0 = (float)(n0 | (int)(((c.qh >> e0) & 1u) << 4));
-                v1 = (float)(n1 | (int)(((c.qh >> e1) & 1u) << 4));
+        for (int i = 0; i < 4; i++) {
+            uint32_t lo = wd[i] & 0x0f0f0f0fu, hi = (wd[i] >> 4) & 0x0f0f0f0fu;
+            if (TYPE == kQ5_1) {
+                // fifth bits of elements 4i..4i+3 and 16+4i..: spread 4 bits to bit 4 of each byte
+                uint32_t bl = (c.qh >> (4 * i)) & 15u, bh = (c.qh >> (16 + 4 * i)) & 15u;
+                lo |= ((bl * 0x00204081u) & 0x01010101u) << 4;
+                hi |= ((bh * 0x00204081u) & 0x01010101u) << 4;
             }
-            o[i] = pack2(v0, v1);
+            bytes_to_f16(lo, bias, o[2 * i], o[2 * i + 1]);
+            bytes_to_f16(hi, bias, o[8 + 2 * i], o[8 + 2 * i + 1]);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) d4[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
@@ -158,7 +154,7 @@ struct AFrag {
 
 } // namespace
 
-template <int TYPE, int MODE, int WM, int WN, int TM, int TN>
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD>
 __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int nt, int gm)
 {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
@@ -189,41 +185,55 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     const int nstage = (nblk + 1) >> 1;
     const int m0 = tile_m * BM;
 
-    // ---- loader role (B): chunk ids tid + 256 j
-    int c_row[CPT], c_ch[CPT], c_seg[CPT], c_wrow[CPT];
+    // ---- loader role (B): chunk ids tid + 256 j.  Row pointers are resolved
+    // once; each stage only adds the block offset.
+    const uint8_t *bq[CPT];
+    const uint16_t *bd[CPT], *bm[CPT];
+    const uint32_t *bh[CPT];
+    int b_lds[CPT], b_kb2[CPT];
+    bool b_own[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
         int c = tid + 256 * j;
-        c_row[j] = c < CHUNKS ? c / CH : -1; // -1: no chunk (loads a duplicate, stores nothing)
-        c_ch[j] = c % CH;
-        map_row<MODE, BN>(a, tile_n, c < CHUNKS ? c / CH : 0, c_seg[j], c_wrow[j]);
+        b_own[j] = c < CHUNKS; // threads past the tile load a duplicate and store nothing
+        int rr = b_own[j] ? c / CH : 0, ch = c % CH;
+        int seg, row;
+        map_row<MODE, BN>(a, tile_n, rr, seg, row);
+        const QWeight &w = a.seg[seg];
+        row = min(row, w.rows - 1); // rows past the weight feed unstored columns
+        int half = TYPE == kQ8_0 ? (ch & 1) : 0;
+        b_kb2[j] = TYPE == kQ8_0 ? (ch >> 1) : ch;
+        bq[j] = TYPE == kQ8_0 ? w.qs + (size_t)row * w.cols + 16 * half : w.qs + (size_t)row * (w.cols >> 1);
+        bd[j] = w.d + (size_t)row * nblk;
+        bm[j] = TYPE == kQ5_1 ? w.m + (size_t)row * nblk : nullptr;
+        bh[j] = TYPE == kQ5_1 ? w.qh + (size_t)row * nblk : nullptr;
+        b_lds[j] = rr * LROW + b_kb2[j] * 32 + half * 16 + (half == 0 ? 0 : 0);
+        if (half != 0) b_lds[j] |= 1 << 30; // marks the second half of a Q8_0 block (no scale store)
     }
     auto load_b = [&](int st, BChunk (&br)[CPT]) {
         st = min(st, nstage - 1);
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            int kblk, half;
-            if (TYPE == kQ8_0) {
-                kblk = 2 * st + (c_ch[j] >> 1);
-                half = c_ch[j] & 1;
-            } else {
-                kblk = 2 * st + c_ch[j];
-                half = 0;
+            int kblk = min(2 * st + b_kb2[j], nblk - 1);
+            br[j].q = *(const u32x4 *)(bq[j] + (size_t)kblk * (TYPE == kQ8_0 ? 32 : 16));
+            br[j].d = bd[j][kblk];
+            if (TYPE == kQ5_1) {
+                br[j].m = bm[j][kblk];
+                br[j].qh = bh[j][kblk];
             }
-            load_chunk<TYPE>(a.seg[c_seg[j]], c_wrow[j], kblk, half, nblk, br[j]);
+            br[j].valid = true;
         }
     };
     auto store_b = [&](int buf, const BChunk (&br)[CPT]) {
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            if (c_row[j] < 0) continue;
-            int rr = c_row[j];
-            int kb2 = TYPE == kQ8_0 ? (c_ch[j] >> 1) : c_ch[j];
-            int half = TYPE == kQ8_0 ? (c_ch[j] & 1) : 0;
-            store_chunk<TYPE>(br[j], half, &Bs[buf][rr * LROW + kb2 * 32 + half * 16]);
-            if (half == 0) {
-                Ds[buf][rr * 2 + kb2] = br[j].valid ? h2f(br[j].d) : 0.f;
-                if (TYPE == kQ5_1) Ms[buf][rr * 2 + kb2] = br[j].valid ? h2f(br[j].m) : 0.f;
+            if (!b_own[j]) continue;
+            int off = b_lds[j] & ~(1 << 30);
+            store_chunk<TYPE>(br[j], 0, &Bs[buf][off]);
+            if (!(b_lds[j] >> 30)) {
+                int rr = off / LROW;
+                Ds[buf][rr * 2 + b_kb2[j]] = h2f(br[j].d);
+                if (TYPE == kQ5_1) Ms[buf][rr * 2 + b_kb2[j]] = h2f(br[j].m);
             }
         }
     };
@@ -233,15 +243,17 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     const int rg0 = (m0 >> 4) + wm * TM;
     const int frag_k = 8 * (lane >> 4); // k offset of this lane's B fragment within a block
     const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
+    const uint16_t *a_tile[TM];
+#pragma unroll
+    for (int mi = 0; mi < TM; mi++) a_tile[mi] = a.xt + (size_t)min(rg0 + mi, rg_last) * nblk * 1024 + lane * 8;
     auto load_a = [&](int st, AFrag<TM> &f) {
         st = min(st, nstage - 1);
 #pragma unroll
         for (int mi = 0; mi < TM; mi++) {
-            int rg = min(rg0 + mi, rg_last);
 #pragma unroll
             for (int kb2 = 0; kb2 < 2; kb2++) {
                 int kblk = min(2 * st + kb2, nblk - 1);
-                const uint16_t *tile = a.xt + (((size_t)rg * nblk + kblk) * 2) * 512 + lane * 8;
+                const uint16_t *tile = a_tile[mi] + (size_t)kblk * 1024;
                 f.hi[mi][kb2] = *(const half8_t *)tile;
                 f.lo[mi][kb2] = *(const half8_t *)(tile + 512);
                 if (TYPE == kQ5_1) {
@@ -316,32 +328,34 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
         }
     };
 
-    // ---- prologue: stage 0 decoded into LDS, stages 1 and 2 raw in registers
-    BChunk br0[CPT], br1[CPT];
-    AFrag<TM> fa0, fa1;
-    load_b(0, br0);
-    load_b(1, br1);
-    load_a(0, fa0);
-    store_b(0, br0);
-    load_b(2, br0);
+    // ---- software pipeline.  Ring of U = PD + 1 register slots: A fragments
+    // are loaded PD stages ahead, raw weight chunks PD + 1 stages ahead (they
+    // are decoded into LDS one stage before use).  The loop is unrolled by U
+    // so every ring index is a compile-time constant.
+    constexpr int U = PD + 1;
+    BChunk br[U][CPT];
+    AFrag<TM> fa[U];
+#pragma unroll
+    for (int j = 0; j < PD; j++) load_a(j, fa[j]);
+#pragma unroll
+    for (int j = 0; j <= PD; j++) load_b(j, br[j]);
+    store_b(0, br[0]);
     __syncthreads();
 
-    // Iteration s: compute on stage s (LDS buffer s & 1, A regs), decode stage
-    // s + 1 from its raw registers, refill those registers with stage s + 3.
-    int s = 0;
-    for (; s + 1 < nstage; s += 2) {
-        load_a(s + 1, fa1);
-        compute(s, 0, fa0);
-        store_b(1, br1);
-        load_b(s + 3, br1);
-        __syncthreads();
-        load_a(s + 2, fa0);
-        compute(s + 1, 1, fa1);
-        store_b(0, br0);
-        load_b(s + 4, br0);
-        __syncthreads();
+    // Iteration s: compute stage s (LDS buffer s & 1, A slot s % U), decode
+    // stage s + 1 into the other buffer, refill the freed slots.
+    for (int s0 = 0; s0 < nstage; s0 += U) {
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const int s = s0 + j;
+            if (s >= nstage) break;
+            load_a(s + PD, fa[(j + PD) % U]);
+            compute(s, s & 1, fa[j]);
+            store_b((s + 1) & 1, br[(j + 1) % U]);
+            load_b(s + PD + 1, br[j]);
+            __syncthreads();
+        }
     }
-    if (s < nstage) compute(s, 0, fa0);
 
     // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
     const int row_base = m0 + wm * TM * 16 + 4 * (lane >> 4);
@@ -392,7 +406,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     }
 }
 
-template <int TYPE, int MODE, int WM, int WN, int TM, int TN>
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD>
 static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
 {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
@@ -408,7 +422,7 @@ static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
     int gm = mt <= 8 ? mt : 8;
     int tiles = mt * ncols;
     int grid = (tiles + 7) & ~7;
-    hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
+    hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
     return hipGetLastError();
 }
 
@@ -416,8 +430,11 @@ template <int TYPE, int MODE>
 static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
 {
     // Shape choice by M only changes which rows share a tile, never a result bit.
-    if (a.M <= 512) return launch_cfg<TYPE, MODE, 2, 2, 2, 2>(a, s);
-    return launch_cfg<TYPE, MODE, 4, 1, 2, 8>(a, s);
+#ifdef JEV_GEMM_CFG
+    return JEV_GEMM_CFG(a, s);
+#endif
+    if (a.M <= 512) return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 3>(a, s);
+    return launch_cfg<TYPE, MODE, 4, 1, 2, 8, 1>(a, s);
 }
 
 template <int TYPE>
