@@ -138,6 +138,7 @@ def main():
             "launches": gemm[0] // args.steps,
             "avg_launch_us": round(gemm_avg_ms * 1e3, 2),
             "flops_per_launch": gemm[2] / max(gemm[0], 1),
+            "alg_bytes_per_launch": round(gemm[3] / max(gemm[0], 1)),
         },
         "breakdown_ms_per_step": {
             "gemm": round(gemm[1] / args.steps, 4),
