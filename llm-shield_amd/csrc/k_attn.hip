@@ -10,19 +10,23 @@
 // shared_lo).  Scores are q.k * 1/sqrt(head_dim), softmax runs over exactly the
 // visible keys, and the context is the weighted sum of their values.
 //
-// Prefill / tree kernel (attn_tree_kernel): fp32 MFMA (v_mfma_f32_16x16x4_f32),
-// flash-style online softmax over blocks of 64 *logical* keys.  A block's
-// shape depends only on the query's own visible range, never on which other
-// queries share its tile, so a branch scores exactly as it would alone:
-// the tree pass is bit-identical to running the branches one at a time.
-// Each tile is up to 64 consecutive tokens with one (shared_lo, shared_hi,
-// segment) and consecutive slots; 4 waves take 16 queries each.  K and V
-// blocks are staged in LDS (rows padded to 132 floats: the fragment reads of a
-// wave fall two lanes per bank).
+// Prefill / tree kernel (attn_tree_kernel): flash-style online softmax over
+// blocks of 64 *logical* keys on the fp16 MFMA cores.  A block's shape
+// depends only on the query's own visible range, never on which other queries
+// share its tile, so a branch scores exactly as it would alone: the tree pass
+// is bit-identical to running the branches one at a time.  Each tile is up to
+// 64 consecutive tokens with one (shared_lo, shared_hi, segment) and
+// consecutive slots; 4 waves take 16 queries each.
 //
-//   S^T (16 keys x 16 queries) = K (16 x 128) . Q^T   32 MFMAs per 16 keys
-//   O^T (128 x 16) += V^T (128 x 64) . P^T (64 x 16)  keys taken in the order
-//                                                     the S^T layout holds them
+// Operands are fp16 pairs (x = hi + lo, ~22 bits): every product is three
+// v_mfma_f32_16x16x32_f16 (hi.hi + hi.lo + lo.hi), which keeps fp32-grade
+// scores at a fraction of the fp32-MFMA cost.  The KV cache stays fp32; K and V
+// blocks are split into pairs while being staged in LDS, K as [key][dim] and V
+// transposed to [dim][key] so both operand fragments are vector reads.
+//
+//   S^T (16 keys x 16 queries) = K (16 x 128) . Q^T      12 MFMAs per 16 keys
+//   O^T (128 x 16) += V^T (128 x 64) . P^T (64 x 16)      48 MFMAs per 64 keys,
+//                     keys taken in the order the S^T fragments hold them
 //
 // Decode kernel (attn_decode_kernel): one query per token, split over chunks
 // of 64 logical keys (one wave each: lane = key for the scores, lane = two
@@ -32,19 +36,40 @@
 namespace jev {
 
 namespace {
-constexpr int KB = 64;        // keys per block
-constexpr int KROW = 132;     // padded LDS row (floats)
+constexpr int KB = 64;          // keys per block
+constexpr int KROW = 128 + 8;   // K pair LDS row, halves (padded: conflict-free fragment reads)
+constexpr int VROW = KB + 8;    // transposed V pair LDS row, halves
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split4(float4 v, uint2 &hi, uint2 &lo)
+{
+    uint16_t h0, l0, h1, l1, h2, l2, h3, l3;
+    split_f16(v.x, h0, l0);
+    split_f16(v.y, h1, l1);
+    split_f16(v.z, h2, l2);
+    split_f16(v.w, h3, l3);
+    hi = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16));
+    lo = make_uint2((uint32_t)l0 | ((uint32_t)l1 << 16), (uint32_t)l2 | ((uint32_t)l3 << 16));
+}
+
+__device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
+{
+    uint4 u = make_uint4(a.x, a.y, b.x, b.y);
+    return __builtin_bit_cast(half8_t, u);
+}
 } // namespace
 
-__global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
+__global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
 {
-    __shared__ __attribute__((aligned(16))) float Ks[KB * KROW];
-    __shared__ __attribute__((aligned(16))) float Vs[KB * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t Kh[KB * KROW], Kl[KB * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t Vh[128 * VROW], Vl[128 * VROW];
 
     const AttnTile tile = a.tiles[blockIdx.x];
     const int head = blockIdx.y;
     const int kvh = head / a.group;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4;
     const int qdim = a.n_heads * 128;
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
@@ -57,12 +82,20 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
     const int max_limit = n_sh + (tile.slot0 + tile.n - 1 - tile.segment + 1);
     const int nblocks = (max_limit + KB - 1) / KB;
 
-    // Q^T fragments: qreg[t] = Q[query][4t + lane/16].
-    float qreg[32];
+    // Q^T fragments: dims 32 c + 8 g .. + 7 of this lane's query, as pairs.
+    half8_t qh[4], ql[4];
     {
-        const float *qp = a.q + (size_t)(tile.t0 + (q_ok ? qi : 0)) * qdim + head * 128 + (lane >> 4);
+        const float *qp = a.q + (size_t)(tile.t0 + (q_ok ? qi : 0)) * qdim + head * 128 + 8 * g;
 #pragma unroll
-        for (int t = 0; t < 32; t++) qreg[t] = q_ok ? qp[4 * t] : 0.f;
+        for (int c = 0; c < 4; c++) {
+            float4 v0 = q_ok ? *(const float4 *)(qp + 32 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 v1 = q_ok ? *(const float4 *)(qp + 32 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            uint2 h0, l0, h1, l1;
+            split4(v0, h0, l0);
+            split4(v1, h1, l1);
+            qh[c] = cat4(h0, h1);
+            ql[c] = cat4(l0, l1);
+        }
     }
 
     floatx4 o[8];
@@ -72,27 +105,52 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
 
     for (int b = 0; b < nblocks; b++) {
         __syncthreads();
-        // Stage 64 keys (and values) of logical block b: thread -> (key, quarter row).
+        // Stage K: thread -> (key, quarter row) as pairs in [key][dim].
         {
             int key = tid >> 2, part = tid & 3;
             int kl = b * KB + key;
-            float4 *kd = (float4 *)(Ks + key * KROW + part * 32);
-            float4 *vd = (float4 *)(Vs + key * KROW + part * 32);
+            uint2 hv[8], lv[8];
             if (kl < max_limit) {
                 int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
                 const float4 *ks = (const float4 *)(kbase + (size_t)p * 128 + part * 32);
-                const float4 *vs = (const float4 *)(vbase + (size_t)p * 128 + part * 32);
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    kd[i] = ks[i];
-                    vd[i] = vs[i];
-                }
+                for (int i = 0; i < 8; i++) split4(ks[i], hv[i], lv[i]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    kd[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    vd[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int i = 0; i < 8; i++) hv[i] = lv[i] = make_uint2(0u, 0u);
+            }
+            uint4 *kh4 = (uint4 *)(Kh + key * KROW + part * 32);
+            uint4 *kl4 = (uint4 *)(Kl + key * KROW + part * 32);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kh4[i] = make_uint4(hv[2 * i].x, hv[2 * i].y, hv[2 * i + 1].x, hv[2 * i + 1].y);
+                kl4[i] = make_uint4(lv[2 * i].x, lv[2 * i].y, lv[2 * i + 1].x, lv[2 * i + 1].y);
+            }
+        }
+        // Stage V transposed: thread -> 4 keys x 8 dims, written as [dim][key].
+        {
+            int kg = tid >> 4, dg = tid & 15;
+            float vv[4][8];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                int kl = b * KB + 4 * kg + kk;
+                if (kl < max_limit) {
+                    int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
+                    const float4 *vs = (const float4 *)(vbase + (size_t)p * 128 + 8 * dg);
+                    float4 v0 = vs[0], v1 = vs[1];
+                    vv[kk][0] = v0.x; vv[kk][1] = v0.y; vv[kk][2] = v0.z; vv[kk][3] = v0.w;
+                    vv[kk][4] = v1.x; vv[kk][5] = v1.y; vv[kk][6] = v1.z; vv[kk][7] = v1.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) vv[kk][i] = 0.f;
                 }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                uint2 hv, lv;
+                split4(make_float4(vv[0][i], vv[1][i], vv[2][i], vv[3][i]), hv, lv);
+                *(uint2 *)(Vh + (8 * dg + i) * VROW + 4 * kg) = hv;
+                *(uint2 *)(Vl + (8 * dg + i) * VROW + 4 * kg) = lv;
             }
         }
         __syncthreads();
@@ -102,9 +160,15 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             floatx4 c = floatx4{0.f, 0.f, 0.f, 0.f};
-            const float *kr = Ks + (16 * s + (lane & 15)) * KROW + (lane >> 4);
+            const int row = (16 * s + (lane & 15)) * KROW + 8 * g;
 #pragma unroll
-            for (int t = 0; t < 32; t++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[4 * t], qreg[t], c, 0, 0, 0);
+            for (int cc = 0; cc < 4; cc++) {
+                half8_t kh = *(const half8_t *)(Kh + row + 32 * cc);
+                half8_t kl = *(const half8_t *)(Kl + row + 32 * cc);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[cc], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[cc], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[cc], c, 0, 0, 0);
+            }
             sc[s] = c;
         }
         // Scale, mask (by the logical key index), block max.
@@ -113,7 +177,7 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
         for (int s = 0; s < 4; s++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                int kl = b * KB + 16 * s + 4 * (lane >> 4) + r;
+                int kl = b * KB + 16 * s + 4 * g + r;
                 float v = sc[s][r] * a.scale;
                 v = kl < my_limit ? v : -INFINITY;
                 sc[s][r] = v;
@@ -141,15 +205,24 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
 #pragma unroll
             for (int r = 0; r < 4; r++) o[j][r] = o[j][r] * alpha;
 
-        // O^T += V^T P^T, k-index kk = lane/16 <-> key 16 s + 4 kk + r.
+        // O^T += V^T P^T over two 32-key chunks; k slot (g, i) <-> key
+        // 16 (2 c + i / 4) + 4 g + i % 4, the keys this lane's P values hold.
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int c = 0; c < 2; c++) {
+            uint2 ph0, pl0, ph1, pl1;
+            split4(make_float4(sc[2 * c][0], sc[2 * c][1], sc[2 * c][2], sc[2 * c][3]), ph0, pl0);
+            split4(make_float4(sc[2 * c + 1][0], sc[2 * c + 1][1], sc[2 * c + 1][2], sc[2 * c + 1][3]), ph1, pl1);
+            half8_t bh = cat4(ph0, ph1), bl = cat4(pl0, pl1);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float *vr = Vs + (16 * s + 4 * (lane >> 4) + r) * KROW + (lane & 15);
-#pragma unroll
-                for (int j = 0; j < 8; j++) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * j], sc[s][r], o[j], 0, 0, 0);
+            for (int j = 0; j < 8; j++) {
+                const int row = (16 * j + (lane & 15)) * VROW + 32 * c + 4 * g;
+                half8_t vh = cat4(*(const uint2 *)(Vh + row), *(const uint2 *)(Vh + row + 16));
+                half8_t vl = cat4(*(const uint2 *)(Vl + row), *(const uint2 *)(Vl + row + 16));
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[j], 0, 0, 0);
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, bh, o[j], 0, 0, 0);
             }
+        }
     }
 
     if (q_ok) {
@@ -158,14 +231,11 @@ __global__ __launch_bounds__(256) void attn_tree_kernel(AttnArgs a)
         const int t = tile.t0 + qi, nblk = qdim >> 5;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            int k = head * 128 + 16 * j + 4 * (lane >> 4);
-            uint16_t hi[4], lo[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) split_f16(o[j][r] * inv, hi[r], lo[r]);
-            *(uint2 *)(a.ot + xt_index(t, k, nblk, 0)) =
-                make_uint2((uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16));
-            *(uint2 *)(a.ot + xt_index(t, k, nblk, 1)) =
-                make_uint2((uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16));
+            int k = head * 128 + 16 * j + 4 * g;
+            uint2 hv, lv;
+            split4(make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv), hv, lv);
+            *(uint2 *)(a.ot + xt_index(t, k, nblk, 0)) = hv;
+            *(uint2 *)(a.ot + xt_index(t, k, nblk, 1)) = lv;
         }
     }
 }
