@@ -76,11 +76,29 @@ struct GemmArgs {
     QWeight seg[3];
     int ldy = 0;
     float *y = nullptr;
-    int ksplit = 1;                      // fixed per (N, K); partials at y + z*M*ldy
+    int ksplit = 1;                      // store mode: K in ksplit ranges, partial z at y + z*M*ldy
     uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
     int mode = kGemmStore;
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+// Quant blocks per K split: an even count (whole 64-wide stages), the last
+// split takes the remainder.  Depends on K and the split count only, so a
+// row's partials are the same whatever M is.
+__host__ __device__ inline int gemm_split_blocks(int nblk, int ksplit)
+{
+    return (((nblk + ksplit - 1) / ksplit) + 1) & ~1;
+}
+// K-split count of a store-mode GEMM with N outputs and K inputs: up to 4
+// splits of at least 8 blocks, so that narrow projections of small batches
+// still fill the GPU.  A function of the weight shape only.
+inline int gemm_choose_split(int N, int K)
+{
+    const int nblk = K >> 5;
+    int s = N > 0 ? 12288 / N : 1;
+    s = s < 1 ? 1 : (s > 4 ? 4 : s);
+    while (s > 1 && (nblk / s < 8 || gemm_split_blocks(nblk, s) * (s - 1) >= nblk)) s--;
+    return s;
+}
 // y[m][n] = sum_z partial[z][m][n] (+ res[m][n] if res), z ascending.
 hipError_t launch_reduce_partials(const float *partial, int ksplit, int M, int N, float *y, hipStream_t s);
 
@@ -103,7 +121,9 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 struct NormArgs {
     int T = 0, D = 0;
     float *h = nullptr;
-    const float *add = nullptr;
+    const float *add = nullptr;    // nadd K-split partials, add_stride floats apart
+    int nadd = 1;
+    size_t add_stride = 0;
     bool store_h = true;           // write h + add back into h
     const float *w = nullptr;
     float eps = 1e-5f;
@@ -125,6 +145,8 @@ struct RopeArgs {
     int T = 0, n_heads = 0, n_kv = 0, hd = 128, half = 64;
     const float *q_in = nullptr, *k_in = nullptr, *v_in = nullptr;
     int ld_in = 0;
+    int nin = 1;            // K-split partials of the inputs, in_stride floats apart
+    size_t in_stride = 0;
     float *q_out = nullptr; // [T][qdim]
     float *kc = nullptr, *vc = nullptr; // layer base: [kvh][cap][hd]
     int cap = 0;

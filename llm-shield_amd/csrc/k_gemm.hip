@@ -34,6 +34,8 @@
 // (144 B) so 16-byte fragment reads of 8 lanes hit distinct banks.
 #include "jev_dev.h"
 
+#include <type_traits>
+
 namespace jev {
 
 namespace {
@@ -61,6 +63,52 @@ struct Geo {
     static constexpr int EL = TYPE == kQ8_0 ? 16 : 32; // elements per chunk
 };
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resource over [p, p + bytes): offsets past the end read zeros.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Loader chunk c of a tile -> (segment, tile row rr, chunk-in-row ch).  For
+// SwiGLU the tile interleaves 16-row groups of gate (segment 0) and up
+// (segment 1) weight rows; chunks are numbered segment-major so the 64 chunks
+// of a wave always lie in one segment (CHUNKS / 2 is a multiple of 64).
+template <int MODE, int BN, int CHUNKS, int CH>
+__device__ __forceinline__ void chunk_of(const GemmArgs &a, int tile_n, int c, int &seg, int &rr, int &ch)
+{
+    if (MODE == kGemmSwiGlu) {
+        seg = c / (CHUNKS / 2);
+        int lc = c % (CHUNKS / 2);
+        int rl = lc / CH;
+        ch = lc % CH;
+        rr = (2 * (rl >> 4) + seg) * 16 + (rl & 15);
+    } else {
+        // the whole tile lies in one segment (segments but the last tile exactly)
+        int n0 = tile_n * BN;
+        int s = 0, start = 0;
+        while (s + 1 < a.nseg && n0 >= start + a.seg[s].rows) {
+            start += a.seg[s].rows;
+            s++;
+        }
+        seg = s;
+        rr = c / CH;
+        ch = c % CH;
+    }
+}
+
+// Weight row (within its segment) of tile row rr.
+template <int MODE, int BN>
+__device__ __forceinline__ int chunk_row(const GemmArgs &a, int tile_n, int seg, int rr)
+{
+    if (MODE == kGemmSwiGlu) return tile_n * (BN / 2) + (rr >> 5) * 16 + (rr & 15);
+    int start = 0;
+    for (int s = 0; s < seg; s++) start += a.seg[s].rows;
+    return tile_n * BN - start + rr;
+}
+
+// Segment and local row of tile column rr (epilogue).
 template <int MODE, int BN>
 __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, int &seg, int &row)
 {
@@ -162,15 +210,21 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     constexpr int CHUNKS = BN * CH;
     constexpr int CPT = (CHUNKS + 255) / 256;
     constexpr int NG = TN < 4 ? TN : 4; // N tiles per partial group
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LROW];
-    __shared__ float Ds[2][BN * 2];
-    __shared__ float Ms[2][TYPE == kQ5_1 ? BN * 2 : 1];
+    // One spare chunk / scale slot past each tile: loaders with nothing to
+    // store write there, so no store (and no wait on its load) is conditional.
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LROW + 32];
+    __shared__ float Ds[2][BN * 2 + 1];
+    __shared__ float Ms[2][TYPE == kQ5_1 ? BN * 2 + 1 : 1];
 
     // ---- tile of this workgroup: contiguous per-XCD runs of a grouped order
     const int total = gridDim.x;
     const int per_xcd = total >> 3;
     const int L = blockIdx.x;
-    const int Lp = (L & 7) * per_xcd + (L >> 3);
+    int Lp = (L & 7) * per_xcd + (L >> 3);
+    // K split z (partials of store-mode GEMMs): whole runs of the tile order
+    const int tiles8 = total / a.ksplit;
+    const int z = Lp / tiles8;
+    Lp -= z * tiles8;
     const int group = gm * nt;
     const int first_m = (Lp / group) * gm;
     const int gsz = min(mt - first_m, gm);
@@ -182,44 +236,60 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int M = a.M, K = a.K, nblk = K >> 5;
-    const int nstage = (nblk + 1) >> 1;
+    // this split's K blocks: [kb_begin, kb_begin + nb)
+    const int nb_per = gemm_split_blocks(nblk, a.ksplit);
+    const int kb_begin = z * nb_per;
+    const int nb = min(nblk - kb_begin, nb_per);
+    const int nstage = (nb + 1) >> 1;
     const int m0 = tile_m * BM;
 
-    // ---- loader role (B): chunk ids tid + 256 j.  Row pointers are resolved
-    // once; each stage only adds the block offset.
-    const uint8_t *bq[CPT];
-    const uint16_t *bd[CPT], *bm[CPT];
-    const uint32_t *bh[CPT];
-    int b_lds[CPT], b_kb2[CPT];
-    bool b_own[CPT];
+    // ---- loader role (B): chunk ids tid + 256 j.  Every load is a buffer
+    // load: a scalar resource for the chunk's weight tensor (uniform across
+    // the wave), a per-lane byte offset fixed for the whole K loop, and a
+    // scalar per-stage offset.  No per-stage vector address arithmetic.
+    rsrc_t rq[CPT], rd[CPT], rm[CPT], rh[CPT];
+    uint32_t vq[CPT], vd[CPT];
+    int b_lds[CPT], b_ds[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
         int c = tid + 256 * j;
-        b_own[j] = c < CHUNKS; // threads past the tile load a duplicate and store nothing
-        int rr = b_own[j] ? c / CH : 0, ch = c % CH;
-        int seg, row;
-        map_row<MODE, BN>(a, tile_n, rr, seg, row);
+        const bool own = c < CHUNKS; // threads past the tile load a duplicate and store it in the spare slot
+        int cc = own ? c : 0;
+        int seg, rr, ch;
+        chunk_of<MODE, BN, CHUNKS, Geo<TYPE>::CH>(a, tile_n, cc, seg, rr, ch);
+        seg = __builtin_amdgcn_readfirstlane(seg);
         const QWeight &w = a.seg[seg];
+        int row = chunk_row<MODE, BN>(a, tile_n, seg, rr);
         row = min(row, w.rows - 1); // rows past the weight feed unstored columns
         int half = TYPE == kQ8_0 ? (ch & 1) : 0;
-        b_kb2[j] = TYPE == kQ8_0 ? (ch >> 1) : ch;
-        bq[j] = TYPE == kQ8_0 ? w.qs + (size_t)row * w.cols + 16 * half : w.qs + (size_t)row * (w.cols >> 1);
-        bd[j] = w.d + (size_t)row * nblk;
-        bm[j] = TYPE == kQ5_1 ? w.m + (size_t)row * nblk : nullptr;
-        bh[j] = TYPE == kQ5_1 ? w.qh + (size_t)row * nblk : nullptr;
-        b_lds[j] = rr * LROW + b_kb2[j] * 32 + half * 16 + (half == 0 ? 0 : 0);
-        if (half != 0) b_lds[j] |= 1 << 30; // marks the second half of a Q8_0 block (no scale store)
+        const int kb2 = TYPE == kQ8_0 ? (ch >> 1) : ch;
+        const uint32_t rowb = TYPE == kQ8_0 ? (uint32_t)w.cols : (uint32_t)(w.cols >> 1);
+        rq[j] = make_rsrc(w.qs, (uint32_t)w.rows * rowb);
+        rd[j] = make_rsrc(w.d, (uint32_t)w.rows * nblk * 2);
+        if (TYPE == kQ5_1) {
+            rm[j] = make_rsrc(w.m, (uint32_t)w.rows * nblk * 2);
+            rh[j] = make_rsrc(w.qh, (uint32_t)w.rows * nblk * 4);
+        }
+        vq[j] = (uint32_t)row * rowb + (kb_begin + kb2) * (TYPE == kQ8_0 ? 32 : 16) + 16 * half;
+        vd[j] = ((uint32_t)row * nblk + kb_begin + kb2) * 2;
+        b_lds[j] = own ? rr * LROW + kb2 * 32 + half * 16 : BN * LROW;
+        // the first half of a Q8_0 block stores the scale, the second the spare slot
+        b_ds[j] = own && half == 0 ? rr * 2 + kb2 : BN * 2;
     }
+    // A stage past the end reloads the last one; an odd block count makes the
+    // last stage's second block read one block past its split (the next
+    // split's first block, the next row, or zeros past the tensor), which only
+    // feeds the skipped second half.
     auto load_b = [&](int st, BChunk (&br)[CPT]) {
         st = min(st, nstage - 1);
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            int kblk = min(2 * st + b_kb2[j], nblk - 1);
-            br[j].q = *(const u32x4 *)(bq[j] + (size_t)kblk * (TYPE == kQ8_0 ? 32 : 16));
-            br[j].d = bd[j][kblk];
+            const int kb0 = 2 * st;
+            br[j].q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[j], vq[j], kb0 * (TYPE == kQ8_0 ? 32 : 16), 0));
+            br[j].d = __builtin_amdgcn_raw_buffer_load_b16(rd[j], vd[j], kb0 * 2, 0);
             if (TYPE == kQ5_1) {
-                br[j].m = bm[j][kblk];
-                br[j].qh = bh[j][kblk];
+                br[j].m = __builtin_amdgcn_raw_buffer_load_b16(rm[j], vd[j], kb0 * 2, 0);
+                br[j].qh = __builtin_amdgcn_raw_buffer_load_b32(rh[j], vd[j] * 2, kb0 * 4, 0);
             }
             br[j].valid = true;
         }
@@ -227,14 +297,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     auto store_b = [&](int buf, const BChunk (&br)[CPT]) {
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            if (!b_own[j]) continue;
-            int off = b_lds[j] & ~(1 << 30);
-            store_chunk<TYPE>(br[j], 0, &Bs[buf][off]);
-            if (!(b_lds[j] >> 30)) {
-                int rr = off / LROW;
-                Ds[buf][rr * 2 + b_kb2[j]] = h2f(br[j].d);
-                if (TYPE == kQ5_1) Ms[buf][rr * 2 + b_kb2[j]] = h2f(br[j].m);
-            }
+            store_chunk<TYPE>(br[j], 0, &Bs[buf][b_lds[j]]);
+            Ds[buf][b_ds[j]] = h2f(br[j].d);
+            if (TYPE == kQ5_1) Ms[buf][b_ds[j]] = h2f(br[j].m);
         }
     };
 
@@ -243,23 +308,31 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     const int rg0 = (m0 >> 4) + wm * TM;
     const int frag_k = 8 * (lane >> 4); // k offset of this lane's B fragment within a block
     const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
-    const uint16_t *a_tile[TM];
+    const rsrc_t ra = make_rsrc(a.xt, (uint32_t)(rg_last + 1) * nblk * 2048);
+    uint32_t va[TM];
 #pragma unroll
-    for (int mi = 0; mi < TM; mi++) a_tile[mi] = a.xt + (size_t)min(rg0 + mi, rg_last) * nblk * 1024 + lane * 8;
+    for (int mi = 0; mi < TM; mi++) va[mi] = ((uint32_t)min(rg0 + mi, rg_last) * nblk * 1024 + lane * 8) * 2;
+    rsrc_t rs;
+    uint32_t vs[TM];
+    if (TYPE == kQ5_1) {
+        rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
+#pragma unroll
+        for (int mi = 0; mi < TM; mi++) vs[mi] = (uint32_t)(m0 + wm * TM * 16 + mi * 16 + 4 * (lane >> 4)) * nblk * 4;
+    }
     auto load_a = [&](int st, AFrag<TM> &f) {
         st = min(st, nstage - 1);
 #pragma unroll
         for (int mi = 0; mi < TM; mi++) {
 #pragma unroll
             for (int kb2 = 0; kb2 < 2; kb2++) {
-                int kblk = min(2 * st + kb2, nblk - 1);
-                const uint16_t *tile = a_tile[mi] + (size_t)kblk * 1024;
-                f.hi[mi][kb2] = *(const half8_t *)tile;
-                f.lo[mi][kb2] = *(const half8_t *)(tile + 512);
+                const int kblk = kb_begin + min(2 * st + kb2, nb - 1);
+                f.hi[mi][kb2] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi], kblk * 2048, 0));
+                f.lo[mi][kb2] = __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi] + 1024, kblk * 2048, 0));
                 if (TYPE == kQ5_1) {
-                    int crow = m0 + wm * TM * 16 + mi * 16 + 4 * (lane >> 4);
+                    // rows past M read zeros (outside the buffer) and are never stored
 #pragma unroll
-                    for (int r = 0; r < 4; r++) f.s[mi][kb2][r] = a.xsum[(size_t)min(crow + r, M - 1) * nblk + kblk];
+                    for (int r = 0; r < 4; r++)
+                        f.s[mi][kb2][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs[mi] + r * nblk * 4, kblk * 4, 0));
                 }
             }
         }
@@ -277,7 +350,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     // block 0 before block 1 for every output.
     constexpr int KS = TM * NG >= 8 ? 1 : 2;
     auto compute = [&](int st, int buf, const AFrag<TM> &f) {
-        const bool second = 2 * st + 1 < nblk;
+        const bool second = 2 * st + 1 < nb;
 #pragma unroll
         for (int k0 = 0; k0 < 2; k0 += KS) {
 #pragma unroll
@@ -342,25 +415,39 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     store_b(0, br[0]);
     __syncthreads();
 
-    // Iteration s: compute stage s (LDS buffer s & 1, A slot s % U), decode
-    // stage s + 1 into the other buffer, refill the freed slots.
-    for (int s0 = 0; s0 < nstage; s0 += U) {
-#pragma unroll
-        for (int j = 0; j < U; j++) {
-            const int s = s0 + j;
-            if (s >= nstage) break;
-            load_a(s + PD, fa[(j + PD) % U]);
-            compute(s, s & 1, fa[j]);
-            store_b((s + 1) & 1, br[(j + 1) % U]);
-            load_b(s + PD + 1, br[j]);
-            __syncthreads();
-        }
+    // Stage s: compute it (LDS buffer s & 1, A slot s % U), decode stage
+    // s + 1 into the other buffer, refill the freed slots.  The loop runs
+    // whole groups of U stages only and the remainder follows it: a loop with
+    // exits inside its body would merge a half-advanced ring into the loop
+    // header, where the compiler would then drain every outstanding load.
+    auto stage = [&](auto jc, int s) {
+        constexpr int j = decltype(jc)::value;
+        load_a(s + PD, fa[(j + PD) % U]);
+        compute(s, s & 1, fa[j]);
+        store_b((s + 1) & 1, br[(j + 1) % U]);
+        load_b(s + PD + 1, br[j]);
+        __syncthreads();
+    };
+    const int ngroups = nstage / U;
+    int s0 = 0;
+    for (int g = 0; g < ngroups; g++, s0 += U) {
+        stage(std::integral_constant<int, 0>{}, s0);
+        if constexpr (U > 1) stage(std::integral_constant<int, 1 % U>{}, s0 + 1);
+        if constexpr (U > 2) stage(std::integral_constant<int, 2 % U>{}, s0 + 2);
+        if constexpr (U > 3) stage(std::integral_constant<int, 3 % U>{}, s0 + 3);
+        static_assert(U <= 4, "ring deeper than the unrolled group");
+    }
+    {
+        const int rem = nstage - s0;
+        if constexpr (U > 1) if (rem > 0) stage(std::integral_constant<int, 0>{}, s0);
+        if constexpr (U > 2) if (rem > 1) stage(std::integral_constant<int, 1 % U>{}, s0 + 1);
+        if constexpr (U > 3) if (rem > 2) stage(std::integral_constant<int, 2 % U>{}, s0 + 2);
     }
 
     // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
     const int row_base = m0 + wm * TM * 16 + 4 * (lane >> 4);
     if (MODE == kGemmStore) {
-        float *y = a.y;
+        float *y = a.y + (size_t)z * M * a.ldy;
         int seg, r0;
         map_row<MODE, BN>(a, tile_n, 0, seg, r0); // segment and local row of the tile's first column
         const QWeight &ws = a.seg[seg];
@@ -421,7 +508,7 @@ static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
     }
     int gm = mt <= 8 ? mt : 8;
     int tiles = mt * ncols;
-    int grid = (tiles + 7) & ~7;
+    int grid = ((tiles + 7) & ~7) * a.ksplit;
     hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
     return hipGetLastError();
 }
@@ -447,7 +534,9 @@ static hipError_t launch_typed(const GemmArgs &a, hipStream_t s)
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s)
 {
     if (a.M <= 0) return hipSuccess;
-    if (a.K % 32 != 0 || a.ksplit != 1) return hipErrorInvalidValue;
+    if (a.K % 32 != 0 || a.ksplit < 1 || a.ksplit > 8) return hipErrorInvalidValue;
+    if (a.ksplit > 1 && (a.mode != kGemmStore || gemm_split_blocks(a.K >> 5, a.ksplit) * (a.ksplit - 1) >= (a.K >> 5)))
+        return hipErrorInvalidValue; // every split non-empty; SwiGLU needs whole sums
     for (int i = 0; i < a.nseg; i++) {
         if (a.seg[i].type != a.seg[0].type || a.seg[i].cols != a.K) return hipErrorInvalidValue;
         // every segment but the last must tile exactly (both tile widths divide 64)

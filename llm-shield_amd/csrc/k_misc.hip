@@ -38,77 +38,97 @@ hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, 
 
 // ------------------------------------------------------------ RMSNorm
 
-// Kernels.RmsNorm (Kernels.cs:25-60) as one workgroup per row: each thread
-// sums the squares of its strided elements in fp32, waves reduce by a fixed
-// butterfly, the four wave sums combine in double; then
-// scale = 1 / sqrt((float)(sum / n) + eps) and y = (x * scale) * w.
-// With `add`, the residual step h += add (Kernels.Add) comes first.
-constexpr int kNormSumMax = 8192;
+// Kernels.RmsNorm (Kernels.cs:25-60) with one wave per row.  Lane l holds
+// the 8-element groups g = l + 64 i of the row in registers, so the row is
+// read once and every operand-tile store is 16 bytes.  Each lane sums its
+// squares in fp32 in group order, a fixed butterfly adds the lanes; then
+// scale = 1 / sqrt(sum / n + eps) and y = (x * scale) * w.  With `add`, the
+// residual step h += add (Kernels.Add) comes first, where add is the sum of
+// `nadd` K-split partials taken in split order.
+constexpr int kNormGroups = 16; // groups of 8 per lane: D <= 8192
 
-__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
+__global__ __launch_bounds__(64) void rmsnorm_kernel(NormArgs a)
 {
-    __shared__ double wsum[4];
-    int t = blockIdx.x;
-    int row = a.rows ? a.rows[t] : t;
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const int row = a.rows ? a.rows[t] : t;
+    const int ng = a.D >> 3, nblk = a.D >> 5;
     float *h = a.h + (size_t)row * a.D;
     const float *add = a.add ? a.add + (size_t)row * a.D : nullptr;
+    float x[kNormGroups][8];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < a.D; i += 256) {
-        float v = h[i];
-        if (add) {
-            v = v + add[i];
-            if (a.store_h) h[i] = v;
-        }
-        float sq = v * v;
-        ss = ss + sq;
-    }
-    ss = warp_sum(ss);
-    int wv = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) wsum[wv] = (double)ss;
-    __syncthreads();
-    double sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    float scale = 1.0f / sqrtf((float)(sum / a.D) + a.eps);
-    const int nblk = a.D >> 5;
-    if (a.out32) {
-        for (int i = threadIdx.x; i < a.D; i += 256) {
-            float x = add && !a.store_h ? h[i] + add[i] : h[i];
-            float v = x * scale;
-            a.out32[(size_t)t * a.D + i] = v * a.w[i];
-        }
-    }
-    if (a.ot) {
-        // eight consecutive k per thread: one 16-byte store per part
-        __shared__ float stage[kNormSumMax];
-        for (int g = threadIdx.x; g < (a.D >> 3); g += 256) {
-            uint32_t hv[4], lv[4];
 #pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                int i = 8 * g + j;
-                float x0 = add && !a.store_h ? h[i] + add[i] : h[i];
-                float x1 = add && !a.store_h ? h[i + 1] + add[i + 1] : h[i + 1];
-                float v0 = x0 * scale, v1 = x1 * scale;
-                float y0 = v0 * a.w[i], y1 = v1 * a.w[i + 1];
-                uint16_t h0, l0, h1, l1;
-                split_f16(y0, h0, l0);
-                split_f16(y1, h1, l1);
-                hv[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                lv[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-                if (a.xsum) {
-                    stage[i] = h2f(h0) + h2f(l0);
-                    stage[i + 1] = h2f(h1) + h2f(l1);
+    for (int i = 0; i < kNormGroups; i++) {
+        const int g = lane + 64 * i;
+        if (64 * i >= ng) break; // uniform: no lane has a group this far
+        if (g < ng) {
+            float4 v0 = *(const float4 *)(h + 8 * g), v1 = *(const float4 *)(h + 8 * g + 4);
+            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if (add) {
+                float4 p0 = *(const float4 *)(add + 8 * g), p1 = *(const float4 *)(add + 8 * g + 4);
+                float s8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                for (int z = 1; z < a.nadd; z++) {
+                    const float *pz = add + (size_t)z * a.add_stride + 8 * g;
+                    float4 q0 = *(const float4 *)pz, q1 = *(const float4 *)(pz + 4);
+                    s8[0] = s8[0] + q0.x; s8[1] = s8[1] + q0.y; s8[2] = s8[2] + q0.z; s8[3] = s8[3] + q0.w;
+                    s8[4] = s8[4] + q1.x; s8[5] = s8[5] + q1.y; s8[6] = s8[6] + q1.z; s8[7] = s8[7] + q1.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = v[j] + s8[j];
+                if (a.store_h) {
+                    *(float4 *)(h + 8 * g) = make_float4(v[0], v[1], v[2], v[3]);
+                    *(float4 *)(h + 8 * g + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 }
             }
-            *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-            *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 1)) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                x[i][j] = v[j];
+                float sq = v[j] * v[j];
+                ss = ss + sq;
+            }
+        }
+    }
+    ss = warp_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)a.D + a.eps);
+#pragma unroll
+    for (int i = 0; i < kNormGroups; i++) {
+        const int g = lane + 64 * i;
+        if (64 * i >= ng) break;
+        float y[8];
+        float bsum = 0.f;
+        if (g < ng) {
+            float4 w0 = *(const float4 *)(a.w + 8 * g), w1 = *(const float4 *)(a.w + 8 * g + 4);
+            float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                float v = x[i][j] * scale;
+                y[j] = v * w[j];
+            }
+            if (a.out32) {
+                float *o = a.out32 + (size_t)t * a.D + 8 * g;
+                *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
+                *(float4 *)(o + 4) = make_float4(y[4], y[5], y[6], y[7]);
+            }
+            if (a.ot) {
+                uint32_t hv[4], lv[4];
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    uint16_t h0, l0, h1, l1;
+                    split_f16(y[j], h0, l0);
+                    split_f16(y[j + 1], h1, l1);
+                    hv[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    lv[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                    bsum += (h2f(h0) + h2f(l0)) + (h2f(h1) + h2f(l1));
+                }
+                *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+                *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 1)) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+            }
         }
         if (a.xsum) {
-            // per-32 block sums of the (hi + lo) values the GEMM will see
-            __syncthreads();
-            for (int b = threadIdx.x; b < nblk; b += 256) {
-                float s = 0.f;
-                for (int j = 0; j < 32; j++) s += stage[b * 32 + j];
-                a.xsum[(size_t)t * nblk + b] = s;
-            }
+            // per-32 block sums of the (hi + lo) values the GEMM sees: the
+            // block's four groups sit on four neighbouring lanes
+            bsum = bsum + __shfl_xor(bsum, 1, 64);
+            bsum = bsum + __shfl_xor(bsum, 2, 64);
+            if (g < ng && (lane & 3) == 0) a.xsum[(size_t)t * nblk + (g >> 2)] = bsum;
         }
     }
 }
@@ -116,9 +136,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
 hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.ot && (a.D > kNormSumMax || a.D % 32 != 0)) return hipErrorInvalidValue;
+    if (a.D % 32 != 0 || a.D > 8 * 64 * kNormGroups || a.nadd < 1) return hipErrorInvalidValue;
     if (a.xsum && !a.ot) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 
@@ -174,11 +194,23 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
     const float *qi = a.q_in + (size_t)t * a.ld_in;
     const float *ki = a.k_in + (size_t)t * a.ld_in;
     const float *vi = a.v_in + (size_t)t * a.ld_in;
+    // K-split partials of the projection, summed in split order
+    auto in2 = [&](const float *p, int k, float &x0, float &x1) {
+        float2 v = *(const float2 *)(p + k);
+        for (int z = 1; z < a.nin; z++) {
+            float2 u = *(const float2 *)(p + (size_t)z * a.in_stride + k);
+            v.x = v.x + u.x;
+            v.y = v.y + u.y;
+        }
+        x0 = v.x;
+        x1 = v.y;
+    };
     float *qo = a.q_out + (size_t)t * qdim;
     int hpairs = a.hd >> 1;
     for (int p = threadIdx.x; p < (qdim >> 1); p += 256) {
         int i = p % hpairs;
-        float x0 = qi[2 * p], x1 = qi[2 * p + 1];
+        float x0, x1;
+        in2(qi, 2 * p, x0, x1);
         float o0 = x0, o1 = x1;
         if (i < a.half) {
             float c = cs[i], sv = sn[i];
@@ -196,7 +228,8 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
     for (int p = threadIdx.x; p < (kvdim >> 1); p += 256) {
         int i = p % hpairs;
         int h = (2 * p) / a.hd, d = (2 * p) % a.hd;
-        float x0 = ki[2 * p], x1 = ki[2 * p + 1];
+        float x0, x1;
+        in2(ki, 2 * p, x0, x1);
         float o0 = x0, o1 = x1;
         if (i < a.half) {
             float c = cs[i], sv = sn[i];
@@ -208,8 +241,10 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
         kd[0] = o0;
         kd[1] = o1;
         float *vd = a.vc + ((size_t)h * a.cap + slot) * a.hd + d;
-        vd[0] = vi[2 * p];
-        vd[1] = vi[2 * p + 1];
+        float v0, v1;
+        in2(vi, 2 * p, v0, v1);
+        vd[0] = v0;
+        vd[1] = v1;
     }
 }
 

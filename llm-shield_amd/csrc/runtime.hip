@@ -142,6 +142,11 @@ struct jev_ctx {
     int qdim() const { return cfg.n_heads * cfg.head_dim; }
     int kvdim() const { return cfg.n_kv_heads * cfg.head_dim; }
     const QWeight &table() const { return output.base ? output : embd; }
+    // K-split counts of the store-mode projections (GEMM path, two or more
+    // tokens); partials are summed by the kernel that consumes the output.
+    int split_qkv() const { return gemm_choose_split(qdim() + 2 * kvdim(), cfg.hidden); }
+    int split_o() const { return gemm_choose_split(cfg.hidden, qdim()); }
+    int split_down() const { return gemm_choose_split(cfg.hidden, cfg.ffn); }
     size_t layer_stride() const { return (size_t)cfg.n_kv_heads * cap * cfg.head_dim; }
 };
 
@@ -308,9 +313,10 @@ int kv_ensure(jev_ctx *c, int required)
 bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a.type == b.type && b.type == c.type; }
 
 // One linear step y = x . W^T over up to three weights sharing x.  T >= 2:
-// MFMA GEMM on the fp16 pair; T == 1: GEMV on fp32 x.
+// MFMA GEMM on the fp16 pair, as `ksplit` K-split partials T * ldy floats
+// apart; T == 1: GEMV on fp32 x (one partial).
 int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xt, const float *xsum,
-           const float *x32, float *y, int ldy)
+           const float *x32, float *y, int ldy, int ksplit)
 {
     double nrows = 0, wbytes = 0;
     for (int i = 0; i < nw; i++) {
@@ -339,6 +345,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
     g.ldy = ldy;
     g.y = y;
+    g.ksplit = ksplit;
     HIP_TRY(launch_gemm(g, c->stream));
     return JEV_OK;
 }
@@ -349,9 +356,10 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
     size_t qkv = (size_t)c->qdim() + 2 * c->kvdim();
     size_t wide = std::max<size_t>({(size_t)f.hidden, (size_t)c->qdim(), (size_t)f.ffn});
     HIP_TRY(c->h.ensure((size_t)T * f.hidden));
-    HIP_TRY(c->y.ensure((size_t)T * qkv));
-    HIP_TRY(c->yo.ensure((size_t)T * f.hidden));
-    HIP_TRY(c->ydown.ensure((size_t)T * f.hidden));
+    const bool multi = T >= 2;
+    HIP_TRY(c->y.ensure((size_t)T * qkv * (multi ? c->split_qkv() : 1)));
+    HIP_TRY(c->yo.ensure((size_t)T * f.hidden * (multi ? c->split_o() : 1)));
+    HIP_TRY(c->ydown.ensure((size_t)T * f.hidden * (multi ? c->split_down() : 1)));
     HIP_TRY(c->q.ensure((size_t)T * c->qdim()));
     HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + 1));
     if (T == 1) {
@@ -531,6 +539,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     (void)q51;
     hipStream_t s = c->stream;
 
+    const int s_o = T >= 2 ? c->split_o() : 1, s_down = T >= 2 ? c->split_down() : 1;
+    const size_t stride_d = (size_t)T * D; // floats between partials of yo / ydown
     HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
     for (int l = 0; l < f.n_layers; l++) {
         if (c->cancel.exchange(0)) return fail(JEV_ECANCELED, "the forward pass was cancelled at layer %d", l);
@@ -544,6 +554,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         na.D = D;
         na.h = c->h.p;
         na.add = l > 0 ? c->ydown.p : nullptr;
+        na.nadd = s_down;
+        na.add_stride = stride_d;
         na.w = L.attn_norm;
         na.eps = f.rms_eps;
         if (T == 1) na.out32 = c->x32.p;
@@ -556,16 +568,18 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         // Q | K | V
         const int ldqkv = qdim + 2 * kvdim;
         bool fuse = same_type3(L.q, L.k, L.v) && (T == 1 || (qdim % 128 == 0 && kvdim % 128 == 0));
+        // separate projections share y's columns, so they are not split
+        const int s_qkv = T >= 2 && fuse ? c->split_qkv() : 1;
         if (fuse) {
             const QWeight *ws[3] = {&L.q, &L.k, &L.v};
-            int rc = linear(c, T, ws, 3, c->xt.p, c->xsum.p, c->x32.p, c->y.p, ldqkv);
+            int rc = linear(c, T, ws, 3, c->xt.p, c->xsum.p, c->x32.p, c->y.p, ldqkv, s_qkv);
             if (rc) return rc;
         } else {
             const QWeight *wq[1] = {&L.q}, *wk[1] = {&L.k}, *wv[1] = {&L.v};
             float *yq = c->y.p, *yk = c->y.p + qdim, *yv = c->y.p + qdim + kvdim;
-            int rc = linear(c, T, wq, 1, c->xt.p, c->xsum.p, c->x32.p, yq, ldqkv);
-            if (!rc) rc = linear(c, T, wk, 1, c->xt.p, c->xsum.p, c->x32.p, yk, ldqkv);
-            if (!rc) rc = linear(c, T, wv, 1, c->xt.p, c->xsum.p, c->x32.p, yv, ldqkv);
+            int rc = linear(c, T, wq, 1, c->xt.p, c->xsum.p, c->x32.p, yq, ldqkv, 1);
+            if (!rc) rc = linear(c, T, wk, 1, c->xt.p, c->xsum.p, c->x32.p, yk, ldqkv, 1);
+            if (!rc) rc = linear(c, T, wv, 1, c->xt.p, c->xsum.p, c->x32.p, yv, ldqkv, 1);
             if (rc) return rc;
         }
         if (T == 1 && !fuse) {
@@ -583,6 +597,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.k_in = c->y.p + qdim;
         ra.v_in = c->y.p + qdim + kvdim;
         ra.ld_in = ldqkv;
+        ra.nin = s_qkv;
+        ra.in_stride = (size_t)T * ldqkv;
         ra.q_out = c->q.p;
         ra.kc = kc;
         ra.vc = vc;
@@ -640,13 +656,14 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         }
         {
             const QWeight *wo[1] = {&L.o};
-            int rc = linear(c, T, wo, 1, c->xt.p, c->xsum.p, c->ctx32.p, c->yo.p, D);
+            int rc = linear(c, T, wo, 1, c->xt.p, c->xsum.p, c->ctx32.p, c->yo.p, D, s_o);
             if (rc) return rc;
         }
 
         // FFN norm (+ attention residual)
         NormArgs nf = na;
         nf.add = c->yo.p;
+        nf.nadd = s_o;
         nf.w = L.ffn_norm;
         nf.xsum = (T > 1 && L.gate.type == kQ5_1) ? c->xsum.p : nullptr;
         HIP_TRY(launch_rmsnorm(nf, s));
@@ -680,7 +697,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         }
         {
             const QWeight *wd[1] = {&L.down};
-            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D);
+            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down);
             if (rc) return rc;
         }
     }
@@ -694,6 +711,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     fn.D = D;
     fn.h = c->h.p;
     fn.add = c->ydown.p;
+    fn.nadd = s_down;
+    fn.add_stride = stride_d;
     fn.store_h = false;
     fn.w = c->out_norm;
     fn.eps = f.rms_eps;
@@ -1251,7 +1270,8 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
     float *dx = nullptr, *dy = nullptr, *dsum = nullptr;
     uint16_t *xt = nullptr;
     hipError_t e = hipMalloc((void **)&dx, nx * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * sizeof(float));
+    const int ksplit = tokens >= 2 ? gemm_choose_split((int)rows, (int)cols) : 1;
+    if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * ksplit * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess && tokens >= 2) {
         size_t t16 = ((size_t)tokens + 15) & ~(size_t)15;
@@ -1268,7 +1288,9 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
             g.seg[0] = w;
             g.ldy = (int)rows;
             g.y = dy;
+            g.ksplit = ksplit;
             e = launch_gemm(g, nullptr);
+            if (e == hipSuccess && ksplit > 1) e = launch_reduce_partials(dy, ksplit, tokens, (int)rows, dy, nullptr);
         }
     } else if (e == hipSuccess) {
         GemvArgs g;
