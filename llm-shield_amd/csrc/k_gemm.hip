@@ -202,8 +202,10 @@ struct AFrag {
 
 } // namespace
 
-template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD>
-__global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int nt, int gm)
+// KS: quant blocks whose partials are in flight together (1 or 2); OCC:
+// waves per SIMD the register budget is cut for.
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD, int KS, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, int nt, int gm)
 {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
     constexpr int CH = Geo<TYPE>::CH;
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     // (+ m * sum(x)).  KS blocks' partials are in flight together so each MFMA
     // result is consumed several MFMAs after it issues; the FMAs still apply
     // block 0 before block 1 for every output.
-    constexpr int KS = TM * NG >= 8 ? 1 : 2;
+    static_assert(KS == 1 || KS == 2, "one or two blocks in flight");
     auto compute = [&](int st, int buf, const AFrag<TM> &f) {
         const bool second = 2 * st + 1 < nb;
 #pragma unroll
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q_kernel(GemmArgs a, int mt, int 
     }
 }
 
-template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD>
+template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD, int KS, int OCC>
 static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
 {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
@@ -509,7 +511,7 @@ static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
     int gm = mt <= 8 ? mt : 8;
     int tiles = mt * ncols;
     int grid = ((tiles + 7) & ~7) * a.ksplit;
-    hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
+    hipLaunchKernelGGL((gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD, KS, OCC>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
     return hipGetLastError();
 }
 
@@ -520,8 +522,8 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
 #ifdef JEV_GEMM_CFG
     return JEV_GEMM_CFG(a, s);
 #endif
-    if (a.M <= 512) return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 3>(a, s);
-    return launch_cfg<TYPE, MODE, 4, 1, 2, 8, 1>(a, s);
+    if (a.M <= 512) return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
+    return launch_cfg<TYPE, MODE, 4, 1, 2, 8, 1, 1, 2>(a, s);
 }
 
 template <int TYPE>

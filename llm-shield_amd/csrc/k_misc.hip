@@ -38,97 +38,112 @@ hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, 
 
 // ------------------------------------------------------------ RMSNorm
 
-// Kernels.RmsNorm (Kernels.cs:25-60) with one wave per row.  Lane l holds
-// the 8-element groups g = l + 64 i of the row in registers, so the row is
-// read once and every operand-tile store is 16 bytes.  Each lane sums its
-// squares in fp32 in group order, a fixed butterfly adds the lanes; then
+// Kernels.RmsNorm (Kernels.cs:25-60), one workgroup per row.  Thread t
+// owns the float4 groups g = t + 256 i of the row; every load of the row (h
+// and the K-split partials of `add`) is issued before the first use, so a row
+// costs one memory round trip.  Squares are summed per thread in group order,
+// then by a fixed butterfly per wave and the four wave sums in order;
 // scale = 1 / sqrt(sum / n + eps) and y = (x * scale) * w.  With `add`, the
 // residual step h += add (Kernels.Add) comes first, where add is the sum of
-// `nadd` K-split partials taken in split order.
-constexpr int kNormGroups = 16; // groups of 8 per lane: D <= 8192
+// `nadd` partials taken in split order.
+constexpr int kNormIters = 8;   // float4 groups per thread: D <= 8192
+constexpr int kNormParts = 4;   // K-split partials
 
-__global__ __launch_bounds__(64) void rmsnorm_kernel(NormArgs a)
+__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
 {
-    const int t = blockIdx.x, lane = threadIdx.x;
+    __shared__ float wsum[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
     const int row = a.rows ? a.rows[t] : t;
-    const int ng = a.D >> 3, nblk = a.D >> 5;
-    float *h = a.h + (size_t)row * a.D;
-    const float *add = a.add ? a.add + (size_t)row * a.D : nullptr;
-    float x[kNormGroups][8];
-    float ss = 0.f;
+    const int ng = a.D >> 2, nblk = a.D >> 5;
+    float4 *h4 = (float4 *)(a.h + (size_t)row * a.D);
+    const float4 *add4 = a.add ? (const float4 *)(a.add + (size_t)row * a.D) : nullptr;
+    const size_t pstride = a.add_stride >> 2;
+    float4 x[kNormIters], p[kNormParts][kNormIters];
 #pragma unroll
-    for (int i = 0; i < kNormGroups; i++) {
-        const int g = lane + 64 * i;
-        if (64 * i >= ng) break; // uniform: no lane has a group this far
-        if (g < ng) {
-            float4 v0 = *(const float4 *)(h + 8 * g), v1 = *(const float4 *)(h + 8 * g + 4);
-            float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            if (add) {
-                float4 p0 = *(const float4 *)(add + 8 * g), p1 = *(const float4 *)(add + 8 * g + 4);
-                float s8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                for (int z = 1; z < a.nadd; z++) {
-                    const float *pz = add + (size_t)z * a.add_stride + 8 * g;
-                    float4 q0 = *(const float4 *)pz, q1 = *(const float4 *)(pz + 4);
-                    s8[0] = s8[0] + q0.x; s8[1] = s8[1] + q0.y; s8[2] = s8[2] + q0.z; s8[3] = s8[3] + q0.w;
-                    s8[4] = s8[4] + q1.x; s8[5] = s8[5] + q1.y; s8[6] = s8[6] + q1.z; s8[7] = s8[7] + q1.w;
-                }
+    for (int i = 0; i < kNormIters; i++) {
+        if (256 * i >= ng) break;
+        const int g = min(tid + 256 * i, ng - 1); // clamped: out-of-row lanes load and drop
+        x[i] = h4[g];
+    }
+    if (add4) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = v[j] + s8[j];
-                if (a.store_h) {
-                    *(float4 *)(h + 8 * g) = make_float4(v[0], v[1], v[2], v[3]);
-                    *(float4 *)(h + 8 * g + 4) = make_float4(v[4], v[5], v[6], v[7]);
-                }
-            }
+        for (int z = 0; z < kNormParts; z++) {
+            if (z >= a.nadd) break;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                x[i][j] = v[j];
-                float sq = v[j] * v[j];
-                ss = ss + sq;
+            for (int i = 0; i < kNormIters; i++) {
+                if (256 * i >= ng) break;
+                const int g = min(tid + 256 * i, ng - 1);
+                p[z][i] = add4[z * pstride + g];
             }
         }
     }
-    ss = warp_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)a.D + a.eps);
+    float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < kNormGroups; i++) {
-        const int g = lane + 64 * i;
-        if (64 * i >= ng) break;
-        float y[8];
-        float bsum = 0.f;
-        if (g < ng) {
-            float4 w0 = *(const float4 *)(a.w + 8 * g), w1 = *(const float4 *)(a.w + 8 * g + 4);
-            float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    for (int i = 0; i < kNormIters; i++) {
+        if (256 * i >= ng) break;
+        const int g = tid + 256 * i;
+        float4 v = x[i];
+        if (add4) {
+            float4 s4 = p[0][i];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                float v = x[i][j] * scale;
-                y[j] = v * w[j];
+            for (int z = 1; z < kNormParts; z++) {
+                if (z >= a.nadd) break;
+                s4.x = s4.x + p[z][i].x;
+                s4.y = s4.y + p[z][i].y;
+                s4.z = s4.z + p[z][i].z;
+                s4.w = s4.w + p[z][i].w;
             }
-            if (a.out32) {
-                float *o = a.out32 + (size_t)t * a.D + 8 * g;
-                *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
-                *(float4 *)(o + 4) = make_float4(y[4], y[5], y[6], y[7]);
-            }
-            if (a.ot) {
-                uint32_t hv[4], lv[4];
-#pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    uint16_t h0, l0, h1, l1;
-                    split_f16(y[j], h0, l0);
-                    split_f16(y[j + 1], h1, l1);
-                    hv[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                    lv[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-                    bsum += (h2f(h0) + h2f(l0)) + (h2f(h1) + h2f(l1));
-                }
-                *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 0)) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-                *(uint4 *)(a.ot + xt_index(t, 8 * g, nblk, 1)) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
-            }
+            v.x = v.x + s4.x;
+            v.y = v.y + s4.y;
+            v.z = v.z + s4.z;
+            v.w = v.w + s4.w;
+            if (a.store_h && g < ng) h4[g] = v;
         }
-        if (a.xsum) {
-            // per-32 block sums of the (hi + lo) values the GEMM sees: the
-            // block's four groups sit on four neighbouring lanes
-            bsum = bsum + __shfl_xor(bsum, 1, 64);
-            bsum = bsum + __shfl_xor(bsum, 2, 64);
-            if (g < ng && (lane & 3) == 0) a.xsum[(size_t)t * nblk + (g >> 2)] = bsum;
+        x[i] = v;
+        if (g < ng) {
+            float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
+            ss = ss + q0;
+            ss = ss + q1;
+            ss = ss + q2;
+            ss = ss + q3;
+        }
+    }
+    ss = warp_sum(ss);
+    if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+    __syncthreads();
+    const float sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    const float scale = 1.0f / sqrtf(sum / (float)a.D + a.eps);
+    const float4 *w4 = (const float4 *)a.w;
+#pragma unroll
+    for (int i = 0; i < kNormIters; i++) {
+        if (256 * i >= ng) break;
+        const int g = tid + 256 * i;
+        const bool own = g < ng;
+        const float4 w = w4[min(g, ng - 1)];
+        float y[4] = {(x[i].x * scale) * w.x, (x[i].y * scale) * w.y, (x[i].z * scale) * w.z, (x[i].w * scale) * w.w};
+        if (a.out32 && own) *(float4 *)(a.out32 + (size_t)t * a.D + 4 * g) = make_float4(y[0], y[1], y[2], y[3]);
+        if (a.ot) {
+            uint16_t hh[4], ll[4];
+            float bsum = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                split_f16(y[j], hh[j], ll[j]);
+                bsum += h2f(hh[j]) + h2f(ll[j]);
+            }
+            if (own) {
+                *(uint2 *)(a.ot + xt_index(t, 4 * g, nblk, 0)) =
+                    make_uint2((uint32_t)hh[0] | ((uint32_t)hh[1] << 16), (uint32_t)hh[2] | ((uint32_t)hh[3] << 16));
+                *(uint2 *)(a.ot + xt_index(t, 4 * g, nblk, 1)) =
+                    make_uint2((uint32_t)ll[0] | ((uint32_t)ll[1] << 16), (uint32_t)ll[2] | ((uint32_t)ll[3] << 16));
+            }
+            if (a.xsum) {
+                // per-32 block sums of the (hi + lo) values the GEMM sees: a
+                // block's eight groups sit on eight neighbouring lanes
+                bsum = bsum + __shfl_xor(bsum, 1, 64);
+                bsum = bsum + __shfl_xor(bsum, 2, 64);
+                bsum = bsum + __shfl_xor(bsum, 4, 64);
+                if (own && (tid & 7) == 0) a.xsum[(size_t)t * nblk + (g >> 3)] = bsum;
+            }
         }
     }
 }
@@ -136,9 +151,9 @@ __global__ __launch_bounds__(64) void rmsnorm_kernel(NormArgs a)
 hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.D % 32 != 0 || a.D > 8 * 64 * kNormGroups || a.nadd < 1) return hipErrorInvalidValue;
+    if (a.D % 32 != 0 || a.D > 4 * 256 * kNormIters || a.nadd < 1 || a.nadd > kNormParts) return hipErrorInvalidValue;
     if (a.xsum && !a.ot) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -169,13 +184,67 @@ hipError_t launch_block_sums(const uint16_t *xt, int T, int D, float *xsum, hipS
 // ApplyPositionScale on q (MinistralModel.cs:676-682); k and v land in their
 // cache slots (StoreKeys / StoreValues, :649-669).  cos/sin are computed in
 // float from position * freq with the accurate library functions.
+constexpr int kRopeIters = 16; // q pairs per thread: q dims <= 8192
+constexpr int kRopeKv = 4;     // k / v pairs per thread: kv dims <= 2048
+constexpr int kRopeParts = 4;  // K-split partials of the projection
+
 __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
 {
     __shared__ float cs[512], sn[512];
-    int t = blockIdx.x;
-    int pos = a.pos ? a.pos[t] : a.start + t;
-    int slot = a.slot ? a.slot[t] : a.start + t;
-    for (int i = threadIdx.x; i < a.half; i += 256) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int pos = a.pos ? a.pos[t] : a.start + t;
+    const int slot = a.slot ? a.slot[t] : a.start + t;
+    const int qdim = a.n_heads * a.hd, kvdim = a.n_kv * a.hd;
+    const int nq = qdim >> 1, nkv = kvdim >> 1, hpairs = a.hd >> 1;
+    const float2 *qi = (const float2 *)(a.q_in + (size_t)t * a.ld_in);
+    const float2 *ki = (const float2 *)(a.k_in + (size_t)t * a.ld_in);
+    const float2 *vi = (const float2 *)(a.v_in + (size_t)t * a.ld_in);
+    const size_t zs = a.in_stride >> 1;
+    // every load first (clamped indices; lanes past the end drop their value),
+    // the K-split partials summed in split order afterwards
+    float2 qv[kRopeIters], kv[kRopeKv], vv[kRopeKv];
+#pragma unroll
+    for (int i = 0; i < kRopeIters; i++) {
+        if (256 * i >= nq) continue;
+        qv[i] = qi[min(tid + 256 * i, nq - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < kRopeKv; i++) {
+        if (256 * i >= nkv) continue;
+        kv[i] = ki[min(tid + 256 * i, nkv - 1)];
+        vv[i] = vi[min(tid + 256 * i, nkv - 1)];
+    }
+#pragma unroll
+    for (int z = 1; z < kRopeParts; z++) {
+        if (z >= a.nin) continue;
+        float2 uq[kRopeIters], uk[kRopeKv], uv[kRopeKv];
+#pragma unroll
+        for (int i = 0; i < kRopeIters; i++) {
+            if (256 * i >= nq) continue;
+            uq[i] = qi[z * zs + min(tid + 256 * i, nq - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < kRopeKv; i++) {
+            if (256 * i >= nkv) continue;
+            uk[i] = ki[z * zs + min(tid + 256 * i, nkv - 1)];
+            uv[i] = vi[z * zs + min(tid + 256 * i, nkv - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < kRopeIters; i++) {
+            if (256 * i >= nq) continue;
+            qv[i].x = qv[i].x + uq[i].x;
+            qv[i].y = qv[i].y + uq[i].y;
+        }
+#pragma unroll
+        for (int i = 0; i < kRopeKv; i++) {
+            if (256 * i >= nkv) continue;
+            kv[i].x = kv[i].x + uk[i].x;
+            kv[i].y = kv[i].y + uk[i].y;
+            vv[i].x = vv[i].x + uv[i].x;
+            vv[i].y = vv[i].y + uv[i].y;
+        }
+    }
+    for (int i = tid; i < a.half; i += 256) {
         float theta = (float)pos * a.freqs[i];
         cs[i] = cosf(theta) * a.mscale;
         sn[i] = sinf(theta) * a.mscale;
@@ -190,27 +259,13 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
             scaled = true;
         }
     }
-    int qdim = a.n_heads * a.hd, kvdim = a.n_kv * a.hd;
-    const float *qi = a.q_in + (size_t)t * a.ld_in;
-    const float *ki = a.k_in + (size_t)t * a.ld_in;
-    const float *vi = a.v_in + (size_t)t * a.ld_in;
-    // K-split partials of the projection, summed in split order
-    auto in2 = [&](const float *p, int k, float &x0, float &x1) {
-        float2 v = *(const float2 *)(p + k);
-        for (int z = 1; z < a.nin; z++) {
-            float2 u = *(const float2 *)(p + (size_t)z * a.in_stride + k);
-            v.x = v.x + u.x;
-            v.y = v.y + u.y;
-        }
-        x0 = v.x;
-        x1 = v.y;
-    };
-    float *qo = a.q_out + (size_t)t * qdim;
-    int hpairs = a.hd >> 1;
-    for (int p = threadIdx.x; p < (qdim >> 1); p += 256) {
-        int i = p % hpairs;
-        float x0, x1;
-        in2(qi, 2 * p, x0, x1);
+    float2 *qo = (float2 *)(a.q_out + (size_t)t * qdim);
+#pragma unroll
+    for (int it = 0; it < kRopeIters; it++) {
+        if (256 * it >= nq) continue;
+        const int p = tid + 256 * it;
+        const int i = p % hpairs;
+        float x0 = qv[it].x, x1 = qv[it].y;
         float o0 = x0, o1 = x1;
         if (i < a.half) {
             float c = cs[i], sv = sn[i];
@@ -222,14 +277,16 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
             o0 = o0 * qscale;
             o1 = o1 * qscale;
         }
-        qo[2 * p] = o0;
-        qo[2 * p + 1] = o1;
+        if (p < nq) qo[p] = make_float2(o0, o1);
     }
-    for (int p = threadIdx.x; p < (kvdim >> 1); p += 256) {
-        int i = p % hpairs;
-        int h = (2 * p) / a.hd, d = (2 * p) % a.hd;
-        float x0, x1;
-        in2(ki, 2 * p, x0, x1);
+#pragma unroll
+    for (int it = 0; it < kRopeKv; it++) {
+        if (256 * it >= nkv) continue;
+        const int p = tid + 256 * it;
+        if (p < nkv) {
+        const int i = p % hpairs;
+        const int h = (2 * p) / a.hd, d = (2 * p) % a.hd;
+        float x0 = kv[it].x, x1 = kv[it].y;
         float o0 = x0, o1 = x1;
         if (i < a.half) {
             float c = cs[i], sv = sn[i];
@@ -237,20 +294,18 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
             o0 = m0 - m1;
             o1 = m2 + m3;
         }
-        float *kd = a.kc + ((size_t)h * a.cap + slot) * a.hd + d;
-        kd[0] = o0;
-        kd[1] = o1;
-        float *vd = a.vc + ((size_t)h * a.cap + slot) * a.hd + d;
-        float v0, v1;
-        in2(vi, 2 * p, v0, v1);
-        vd[0] = v0;
-        vd[1] = v1;
+        *(float2 *)(a.kc + ((size_t)h * a.cap + slot) * a.hd + d) = make_float2(o0, o1);
+        *(float2 *)(a.vc + ((size_t)h * a.cap + slot) * a.hd + d) = vv[it];
+        }
     }
 }
 
 hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
+    if (a.n_heads * a.hd > 512 * kRopeIters || a.n_kv * a.hd > 512 * kRopeKv || a.nin < 1 || a.nin > kRopeParts ||
+        a.half > 512 || a.hd % 2 != 0)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_store_kernel, dim3(a.T), dim3(256), 0, s, a);
     return hipGetLastError();
 }
