@@ -24,25 +24,25 @@ __device__ __forceinline__ void split_f16(float x, uint16_t &hi, uint16_t &lo)
     lo = __builtin_bit_cast(uint16_t, l);
 }
 
-// One weight element, decoded exactly as Dequantizer does (Dequantizer.cs:
-// Q4_0 :155-182, Q5_1 :240-268, Q8_0 :270-305).  d*q is exact in fp32, so
-// the Q5_1 "+ m" rounds once whether or not it is fused.
-__device__ __forceinline__ float decode_elem(const QWeight &w, int r, int k)
+// One weight element of the tiled layout, decoded exactly as Dequantizer
+// does (Dequantizer.cs: Q4_0 :155-182, Q5_1 :240-268, Q8_0 :270-305).  d*q is
+// exact in fp32, so the Q5_1 "+ m" rounds once whether or not it is fused.
+__device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
 {
-    int nb = w.cols >> 5;
-    int b = k >> 5, j = k & 31;
-    float d = h2f(w.d[(size_t)r * nb + b]);
+    const int rg = row >> 4, r = row & 15, b = k >> 5, kk = k & 31, g = kk >> 3, i = kk & 7, bb = b & 1;
+    const int l = 16 * g + r;
+    const size_t tile = (size_t)rg * tile_kpairs(w.cols) + (b >> 1);
+    const float d = h2f(w.d[tile * 32 + 2 * r + bb]);
     if (w.type == kQ8_0) {
-        int8_t q = (int8_t)w.qs[(size_t)r * w.cols + k];
+        const int8_t q = (int8_t)w.qs[tile * 1024 + 16 * l + 8 * bb + i];
         return (float)q * d;
     }
-    uint8_t byte = w.qs[(size_t)r * (w.cols >> 1) + b * 16 + (j & 15)];
-    int nib = j < 16 ? (byte & 15) : (byte >> 4);
+    const uint8_t byte = w.qs[tile * 512 + 8 * l + 4 * bb + (i & 3)];
+    const int nib = i < 4 ? (byte & 15) : (byte >> 4);
     if (w.type == kQ4_0) return d * (float)(nib - 8);
-    uint32_t qh = w.qh[(size_t)r * nb + b];
-    int q = nib | (int)(((qh >> j) & 1u) << 4);
-    float m = h2f(w.m[(size_t)r * nb + b]);
-    float dq = d * (float)q;
+    const int q = nib | (((w.qh[tile * 128 + 2 * l + bb] >> i) & 1) << 4);
+    const float m = h2f(w.m[tile * 32 + 2 * r + bb]);
+    const float dq = d * (float)q;
     return dq + m;
 }
 
@@ -55,6 +55,39 @@ __device__ __forceinline__ size_t xt_index(int row, int k, int nblk, int part)
 {
     int rg = row >> 4, r = row & 15, b = k >> 5, kk = k & 31;
     return ((((size_t)rg * nblk + b) * 2 + part) * 64 + ((kk >> 3) * 16 + r)) * 8 + (kk & 7);
+}
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resource over [p, p + bytes): offsets past the end read zeros.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Integer quants to fp16 without float conversions: a byte u placed under
+// the exponent byte 0x64 is the fp16 value 1024 + u (exact, ulp 1 in
+// [1024, 2048)); one packed fp16 subtraction of the bias then leaves the
+// integer.  Four values cost one byte permute per pair plus one v_pk_add_f16
+// per pair.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t biased_pair(uint32_t bytes, uint32_t sel)
+{
+    return __builtin_amdgcn_perm(0x64646464u, bytes, sel);
+}
+
+__device__ __forceinline__ uint32_t sub_bias(uint32_t v, _Float16 bias)
+{
+    half2_t h = __builtin_bit_cast(half2_t, v) - half2_t{bias, bias};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four biased bytes -> two fp16 pairs (elements 0,1 and 2,3).
+__device__ __forceinline__ void bytes_to_f16(uint32_t bytes, _Float16 bias, uint32_t &p01, uint32_t &p23)
+{
+    p01 = sub_bias(biased_pair(bytes, 0x04010400u), bias);
+    p23 = sub_bias(biased_pair(bytes, 0x04030402u), bias);
 }
 
 __device__ __forceinline__ float warp_sum(float v)

@@ -18,26 +18,34 @@ int64_t row_bytes(int type, int64_t cols);
 
 // ---------------------------------------------------------------- layout
 //
-// A quantized 2-D weight in HBM, split by field so every kernel load is an
-// aligned vector load (a GGUF block is 34, 24 or 18 bytes, which no 16-byte
-// load can follow):
-//   Q8_0: qs  int8  [rows][cols]        the 32 quants of each block in order
-//         d   fp16  [rows][cols/32]
-//   Q4_0: qs  uint8 [rows][cols/2]      each block's 16 bytes unchanged (byte j =
-//         d   fp16  [rows][cols/32]      element j low nibble, j+16 high nibble)
-//   Q5_1: qs  uint8 [rows][cols/2]      as Q4_0
-//         qh  uint32[rows][cols/32]     the block's fifth bits, unchanged
-//         d,m fp16  [rows][cols/32]
+// A quantized 2-D weight in HBM as "MFMA tiles": rows in groups of 16 and K
+// in pairs of quant blocks (64 elements).  A tile is, in lane order, exactly
+// the B operand of two v_mfma_f32_16x16x32_f16 (one per block): lane
+// l = 16 g + r of a wave owns row r and k = 8 g .. 8 g + 7 of each block, so
+// one wave-wide load of a tile is a single contiguous access.  Tiles are
+// ordered [row group][block pair]; rows pad to a multiple of 16 and blocks to
+// an even count with zero quants and scales.  Per tile:
+//   qs  Q8_0       1024 B: lane l's 16 bytes at 16 l -- 8 int8 of block 0, then 8 of block 1
+//       Q4_0/Q5_1   512 B: lane l's 8 bytes at 8 l -- 4 of block 0, then 4 of block 1; byte i
+//                          of a block's four = element 8g+i (low nibble) | element 8g+i+4 (high)
+//   d   fp16         64 B: row r's two block scales at 4 r
+//   m   fp16 (Q5_1)  64 B: as d
+//   qh  (Q5_1)      128 B: lane l's fifth bits at 2 l + block, bit i = element 8 g + i
+constexpr int kTileRows = 16, kTileK = 64;
 struct QWeight {
     int type = -1;
     int rows = 0, cols = 0;
     const uint8_t *qs = nullptr;
     const uint16_t *d = nullptr;
     const uint16_t *m = nullptr;
-    const uint32_t *qh = nullptr;
+    const uint8_t *qh = nullptr;
     void *base = nullptr; // owning allocation
     size_t bytes = 0;
 };
+// Tile counts of a weight: row groups and block pairs.
+__host__ __device__ inline int tile_rows(int rows) { return (rows + kTileRows - 1) / kTileRows; }
+__host__ __device__ inline int tile_kpairs(int cols) { return ((cols >> 5) + 1) >> 1; }
+__host__ __device__ inline int tile_qs_bytes(int type) { return type == kQ8_0 ? 1024 : 512; }
 
 // Byte offsets of the fields inside one allocation of the layout above.
 struct QLayout {
@@ -45,7 +53,7 @@ struct QLayout {
 };
 QLayout qlayout(int type, int64_t rows, int64_t cols);
 
-// Host: GGUF blocks (rows x cols) -> the field-split layout in `dst`
+// Host: GGUF blocks (rows x cols) -> the tiled layout in `dst`
 // (qlayout(type, rows, cols).total bytes).  Returns false on a bad type/shape.
 bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *dst, int threads);
 
@@ -111,8 +119,21 @@ struct GemvArgs {
     QWeight seg[3];
     float *y = nullptr;
     int swiglu = 0;
+    int ksplit = 1; // K in ksplit ranges (gemm_split_blocks), partial z at y + z * rows
 };
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
+// GEMV shape rules, functions of the weight shape only.  Many rows: each wave
+// takes 16 rows over the whole K.  Otherwise the four waves of a workgroup
+// share 16 rows, and narrow outputs split K over up to 4 workgroups as well.
+inline bool gemv_rows_mode(int rows) { return (rows + 15) / 16 >= 2048; }
+inline int gemv_choose_split(int rows, int K)
+{
+    if (gemv_rows_mode(rows)) return 1;
+    const int groups = (rows + 15) / 16, nb = K >> 5;
+    int s = 1;
+    while (s < 4 && groups * 4 * s < 2048 && nb / (2 * s * 4) >= 4) s *= 2;
+    return s;
+}
 
 // Row kernels.
 //  rmsnorm: if add != nullptr, h[t] += add[t] first (stored back).  Output is

@@ -48,65 +48,13 @@ struct alignas(16) u32x4 {
 };
 
 
-// One loader chunk: 16 bytes of quants (Q8_0: 16 elements = half a block;
-// Q4_0/Q5_1: one whole block of 32) plus its block's scale fields.
+// One loader chunk: a lane slot of a weight tile -- the quants of one row
+// at k = 8g .. 8g + 7 of both blocks of the stage -- and that row's scales.
 struct BChunk {
-    u32x4 q;
-    uint32_t qh;
-    uint16_t d, m;
-    bool valid;
+    uint4 q;       // Q8_0: 16 bytes; Q4_0 / Q5_1: 8 bytes in .x, .y
+    uint32_t d, m; // two fp16 each (block 0 low half)
+    uint32_t qh;   // Q5_1: two bytes (block 0 low byte)
 };
-
-template <int TYPE>
-struct Geo {
-    static constexpr int CH = TYPE == kQ8_0 ? 4 : 2; // chunks per row per stage
-    static constexpr int EL = TYPE == kQ8_0 ? 16 : 32; // elements per chunk
-};
-
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-// Raw buffer resource over [p, p + bytes): offsets past the end read zeros.
-__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// Loader chunk c of a tile -> (segment, tile row rr, chunk-in-row ch).  For
-// SwiGLU the tile interleaves 16-row groups of gate (segment 0) and up
-// (segment 1) weight rows; chunks are numbered segment-major so the 64 chunks
-// of a wave always lie in one segment (CHUNKS / 2 is a multiple of 64).
-template <int MODE, int BN, int CHUNKS, int CH>
-__device__ __forceinline__ void chunk_of(const GemmArgs &a, int tile_n, int c, int &seg, int &rr, int &ch)
-{
-    if (MODE == kGemmSwiGlu) {
-        seg = c / (CHUNKS / 2);
-        int lc = c % (CHUNKS / 2);
-        int rl = lc / CH;
-        ch = lc % CH;
-        rr = (2 * (rl >> 4) + seg) * 16 + (rl & 15);
-    } else {
-        // the whole tile lies in one segment (segments but the last tile exactly)
-        int n0 = tile_n * BN;
-        int s = 0, start = 0;
-        while (s + 1 < a.nseg && n0 >= start + a.seg[s].rows) {
-            start += a.seg[s].rows;
-            s++;
-        }
-        seg = s;
-        rr = c / CH;
-        ch = c % CH;
-    }
-}
-
-// Weight row (within its segment) of tile row rr.
-template <int MODE, int BN>
-__device__ __forceinline__ int chunk_row(const GemmArgs &a, int tile_n, int seg, int rr)
-{
-    if (MODE == kGemmSwiGlu) return tile_n * (BN / 2) + (rr >> 5) * 16 + (rr & 15);
-    int start = 0;
-    for (int s = 0; s < seg; s++) start += a.seg[s].rows;
-    return tile_n * BN - start + rr;
-}
 
 // Segment and local row of tile column rr (epilogue).
 template <int MODE, int BN>
@@ -133,64 +81,36 @@ __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, i
 // loop free of divergent loads lets the compiler count outstanding loads
 // exactly instead of draining the queue every stage.
 
-// Integer quants to fp16 without float conversions: a byte u placed under
-// the exponent byte 0x64 is the fp16 value 1024 + u (exact, ulp 1 in
-// [1024, 2048)); one packed fp16 subtraction of the bias then leaves the
-// integer.  Four values cost one byte permute per pair plus one v_pk_add_f16
-// per pair.
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t biased_pair(uint32_t bytes, uint32_t sel)
-{
-    return __builtin_amdgcn_perm(0x64646464u, bytes, sel);
-}
-
-__device__ __forceinline__ uint32_t sub_bias(uint32_t v, _Float16 bias)
-{
-    half2_t h = __builtin_bit_cast(half2_t, v) - half2_t{bias, bias};
-    return __builtin_bit_cast(uint32_t, h);
-}
-
-// Four biased bytes -> two fp16 pairs (elements 0,1 and 2,3).
-__device__ __forceinline__ void bytes_to_f16(uint32_t bytes, _Float16 bias, uint32_t &p01, uint32_t &p23)
-{
-    p01 = sub_bias(biased_pair(bytes, 0x04010400u), bias);
-    p23 = sub_bias(biased_pair(bytes, 0x04030402u), bias);
-}
-
-// Decoded quants of one chunk as fp16 integers into the LDS row.
+// Decoded quants of one chunk as fp16 integers: block 0 to dst[0..8),
+// block 1 to dst[32..40) (the LDS row of the chunk's weight row).
 template <int TYPE>
-__device__ __forceinline__ void store_chunk(const BChunk &c, int half, uint16_t *dst)
+__device__ __forceinline__ void store_chunk(const BChunk &c, uint16_t *dst)
 {
-    u32x4 *d4 = (u32x4 *)dst;
-    uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
-    if (TYPE == kQ8_0) {
-        // int8 q: bias by 128 (flip the sign bit), then subtract 1152.
-        uint32_t o[8];
 #pragma unroll
-        for (int i = 0; i < 4; i++) bytes_to_f16(wd[i] ^ 0x80808080u, (_Float16)1152.0f, o[2 * i], o[2 * i + 1]);
-        d4[0] = u32x4{o[0], o[1], o[2], o[3]};
-        d4[1] = u32x4{o[4], o[5], o[6], o[7]};
-    } else {
-        // 32 elements: j < 16 low nibble of byte j, 16 + j high nibble.
-        const _Float16 bias = TYPE == kQ4_0 ? (_Float16)1032.0f : (_Float16)1024.0f;
-        uint32_t o[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t lo = wd[i] & 0x0f0f0f0fu, hi = (wd[i] >> 4) & 0x0f0f0f0fu;
+    for (int bb = 0; bb < 2; bb++) {
+        uint32_t o0, o1, o2, o3;
+        if (TYPE == kQ8_0) {
+            // int8 q: bias by 128 (flip the sign bit), then subtract 1152.
+            const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
+            bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
+            bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
+        } else {
+            // byte i = element i (low nibble) | element i + 4 (high nibble)
+            const uint32_t w = bb ? c.q.y : c.q.x;
+            uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
+            _Float16 bias = (_Float16)1032.0f;
             if (TYPE == kQ5_1) {
-                // fifth bits of elements 4i..4i+3 and 16+4i..: spread 4 bits to bit 4 of each byte
-                uint32_t bl = (c.qh >> (4 * i)) & 15u, bh = (c.qh >> (16 + 4 * i)) & 15u;
-                lo |= ((bl * 0x00204081u) & 0x01010101u) << 4;
-                hi |= ((bh * 0x00204081u) & 0x01010101u) << 4;
+                // fifth bits: spread 4 bits to bit 4 of each byte
+                const uint32_t hb = (c.qh >> (8 * bb)) & 0xffu;
+                n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
+                n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
+                bias = (_Float16)1024.0f;
             }
-            bytes_to_f16(lo, bias, o[2 * i], o[2 * i + 1]);
-            bytes_to_f16(hi, bias, o[8 + 2 * i], o[8 + 2 * i + 1]);
+            bytes_to_f16(n0, bias, o0, o1);
+            bytes_to_f16(n1, bias, o2, o3);
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) d4[i] = u32x4{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+        *(u32x4 *)(dst + 32 * bb) = u32x4{o0, o1, o2, o3};
     }
-    (void)half;
 }
 
 // A fragments of one stage: [mi][kb2] hi and lo.
@@ -208,15 +128,14 @@ template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD, int KS, in
 __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, int nt, int gm)
 {
     constexpr int BM = WM * TM * 16, BN = WN * TN * 16;
-    constexpr int CH = Geo<TYPE>::CH;
-    constexpr int CHUNKS = BN * CH;
+    constexpr int CHUNKS = BN * 4; // 64 lane slots per 16-row weight tile
     constexpr int CPT = (CHUNKS + 255) / 256;
     constexpr int NG = TN < 4 ? TN : 4; // N tiles per partial group
     // One spare chunk / scale slot past each tile: loaders with nothing to
     // store write there, so no store (and no wait on its load) is conditional.
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LROW + 32];
-    __shared__ float Ds[2][BN * 2 + 1];
-    __shared__ float Ms[2][TYPE == kQ5_1 ? BN * 2 + 1 : 1];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LROW + 40];
+    __shared__ float Ds[2][BN * 2 + 2];
+    __shared__ float Ms[2][TYPE == kQ5_1 ? BN * 2 + 2 : 1];
 
     // ---- tile of this workgroup: contiguous per-XCD runs of a grouped order
     const int total = gridDim.x;
@@ -245,63 +164,83 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     const int nstage = (nb + 1) >> 1;
     const int m0 = tile_m * BM;
 
-    // ---- loader role (B): chunk ids tid + 256 j.  Every load is a buffer
-    // load: a scalar resource for the chunk's weight tensor (uniform across
-    // the wave), a per-lane byte offset fixed for the whole K loop, and a
-    // scalar per-stage offset.  No per-stage vector address arithmetic.
+    // ---- loader role (B): chunk c = tid + 256 j is lane slot c % 64 of the
+    // tile row c / 64 of the workgroup's BN weight rows -- one tile per wave,
+    // so its weight (segment) is uniform.  Every load is a buffer load: a
+    // scalar resource, a per-lane offset fixed for the loop and a scalar
+    // per-stage offset; no per-stage vector address arithmetic.
     rsrc_t rq[CPT], rd[CPT], rm[CPT], rh[CPT];
-    uint32_t vq[CPT], vd[CPT];
+    int btile0[CPT]; // first tile of the chunk's row group (uniform)
     int b_lds[CPT], b_ds[CPT];
+    const int slot = tid & 63, sg = slot >> 4, sr = slot & 15;
+    const uint32_t vq = (uint32_t)slot * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * sr, vh = 2 * slot;
+    const int kp_begin = kb_begin >> 1; // kb_begin is even
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
-        int c = tid + 256 * j;
-        const bool own = c < CHUNKS; // threads past the tile load a duplicate and store it in the spare slot
-        int cc = own ? c : 0;
-        int seg, rr, ch;
-        chunk_of<MODE, BN, CHUNKS, Geo<TYPE>::CH>(a, tile_n, cc, seg, rr, ch);
+        const int t = wave + 4 * j; // tile row within the workgroup
+        const bool own = 16 * t < BN; // waves past the tile load a duplicate and store it in the spare slot
+        int seg, rgw;
+        if (MODE == kGemmSwiGlu) {
+            // 16-row groups alternate gate (segment 0) and up (segment 1)
+            seg = t & 1;
+            rgw = tile_n * (BN / 32) + (t >> 1);
+        } else {
+            int s0 = 0, start = 0, n0 = tile_n * BN;
+            while (s0 + 1 < a.nseg && n0 >= start + a.seg[s0].rows) {
+                start += a.seg[s0].rows;
+                s0++;
+            }
+            seg = s0;
+            rgw = (n0 - start) / 16 + t; // segments but the last are whole tiles
+        }
         seg = __builtin_amdgcn_readfirstlane(seg);
         const QWeight &w = a.seg[seg];
-        int row = chunk_row<MODE, BN>(a, tile_n, seg, rr);
-        row = min(row, w.rows - 1); // rows past the weight feed unstored columns
-        int half = TYPE == kQ8_0 ? (ch & 1) : 0;
-        const int kb2 = TYPE == kQ8_0 ? (ch >> 1) : ch;
-        const uint32_t rowb = TYPE == kQ8_0 ? (uint32_t)w.cols : (uint32_t)(w.cols >> 1);
-        rq[j] = make_rsrc(w.qs, (uint32_t)w.rows * rowb);
-        rd[j] = make_rsrc(w.d, (uint32_t)w.rows * nblk * 2);
+        const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
+        const uint32_t tiles = (uint32_t)RG * KP;
+        rq[j] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
+        rd[j] = make_rsrc(w.d, tiles * 64);
         if (TYPE == kQ5_1) {
-            rm[j] = make_rsrc(w.m, (uint32_t)w.rows * nblk * 2);
-            rh[j] = make_rsrc(w.qh, (uint32_t)w.rows * nblk * 4);
+            rm[j] = make_rsrc(w.m, tiles * 64);
+            rh[j] = make_rsrc(w.qh, tiles * 128);
         }
-        vq[j] = (uint32_t)row * rowb + (kb_begin + kb2) * (TYPE == kQ8_0 ? 32 : 16) + 16 * half;
-        vd[j] = ((uint32_t)row * nblk + kb_begin + kb2) * 2;
-        b_lds[j] = own ? rr * LROW + kb2 * 32 + half * 16 : BN * LROW;
-        // the first half of a Q8_0 block stores the scale, the second the spare slot
-        b_ds[j] = own && half == 0 ? rr * 2 + kb2 : BN * 2;
+        // row groups past the weight feed unstored columns
+        btile0[j] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + kp_begin);
+        b_lds[j] = own ? (16 * t + sr) * LROW + 8 * sg : BN * LROW;
+        // lanes of the first k group store the row's two scales, the rest the spare slot
+        b_ds[j] = own && sg == 0 ? (16 * t + sr) * 2 : BN * 2;
     }
-    // A stage past the end reloads the last one; an odd block count makes the
-    // last stage's second block read one block past its split (the next
-    // split's first block, the next row, or zeros past the tensor), which only
-    // feeds the skipped second half.
+    // A stage past the end reloads the last one.  An odd block count leaves
+    // the last stage's second block to the tile padding (zero quants and
+    // scales) or to the next split's first block; either way it only feeds
+    // the skipped second half.
     auto load_b = [&](int st, BChunk (&br)[CPT]) {
         st = min(st, nstage - 1);
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            const int kb0 = 2 * st;
-            br[j].q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[j], vq[j], kb0 * (TYPE == kQ8_0 ? 32 : 16), 0));
-            br[j].d = __builtin_amdgcn_raw_buffer_load_b16(rd[j], vd[j], kb0 * 2, 0);
-            if (TYPE == kQ5_1) {
-                br[j].m = __builtin_amdgcn_raw_buffer_load_b16(rm[j], vd[j], kb0 * 2, 0);
-                br[j].qh = __builtin_amdgcn_raw_buffer_load_b32(rh[j], vd[j] * 2, kb0 * 4, 0);
+            const int tile = btile0[j] + st;
+            if (TYPE == kQ8_0) {
+                br[j].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[j], vq, tile * 1024, 0));
+            } else {
+                uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[j], vq, tile * 512, 0));
+                br[j].q = make_uint4(v.x, v.y, 0u, 0u);
             }
-            br[j].valid = true;
+            br[j].d = __builtin_amdgcn_raw_buffer_load_b32(rd[j], vd, tile * 64, 0);
+            if (TYPE == kQ5_1) {
+                br[j].m = __builtin_amdgcn_raw_buffer_load_b32(rm[j], vd, tile * 64, 0);
+                br[j].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[j], vh, tile * 128, 0);
+            }
         }
     };
     auto store_b = [&](int buf, const BChunk (&br)[CPT]) {
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            store_chunk<TYPE>(br[j], 0, &Bs[buf][b_lds[j]]);
-            Ds[buf][b_ds[j]] = h2f(br[j].d);
-            if (TYPE == kQ5_1) Ms[buf][b_ds[j]] = h2f(br[j].m);
+            store_chunk<TYPE>(br[j], &Bs[buf][b_lds[j]]);
+            Ds[buf][b_ds[j]] = h2f((uint16_t)br[j].d);
+            Ds[buf][b_ds[j] + 1] = h2f((uint16_t)(br[j].d >> 16));
+            if (TYPE == kQ5_1) {
+                Ms[buf][b_ds[j]] = h2f((uint16_t)br[j].m);
+                Ms[buf][b_ds[j] + 1] = h2f((uint16_t)(br[j].m >> 16));
+            }
         }
     };
 

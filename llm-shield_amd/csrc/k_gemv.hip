@@ -2,189 +2,290 @@
 //
 // Replaces QuantMatMul.RunRowsFloat (QuantMatMul.cs:140-176), the path a
 // one-token call (decode, the last-position LM head) takes.  The kernel is
-// bound by streaming the weights from HBM once, so the design goal is bytes in
-// flight, not arithmetic: every lane loads 16 bytes of quants per step
-// (coalesced 1 KiB per wave instruction), decodes them in registers and keeps
-// fp32 FMA chains; x (fp32) is staged once per workgroup in LDS in a
-// lane-interleaved order so the fragment reads are bank-conflict free.
+// bound by streaming the weights from HBM once; the design goal is bytes in
+// flight and few vector instructions per weight byte, so the dot products run
+// on the matrix cores:
 //
-// A lane owns one "unit" per step: 16 elements (half a Q8_0 block) or 32 (a
-// whole Q4_0 / Q5_1 block).  Its partial dot with the integer quants is scaled
-// by the block's d in fp32 (and Q5_1 adds m * sum(x) over the block), then the
-// wave reduces with a fixed butterfly.  x is fp32 throughout: the decode path
-// carries no fp16 rounding.
+//  * x (fp32) is split once per workgroup into an fp16 pair x = hi + lo
+//    (~22 significant bits) and staged in LDS.  It is the MFMA A operand:
+//    row 0 holds hi, row 1 holds lo, rows 2..15 read a zero slot.
+//  * A wave owns 16 weight rows, one tile row of the tiled weight layout.
+//    Per tile (two quant blocks) a lane loads its slot -- the quants of its
+//    row (l % 16) at k = 8 (l / 16) .. + 7 of both blocks, exactly its B
+//    fragments -- as one piece of a contiguous wave-wide load, and decodes
+//    them to exact fp16 integers in registers.
+//  * One v_mfma_f32_16x16x32_f16 per block then yields x_hi . q and x_lo . q
+//    for the 16 rows; the fp32 scale is applied on the vector ALU:
+//    acc += d * (p_hi + p_lo)  (+ m * sum(x) over the block for Q5_1).
+//
+// Narrow projections split K over the workgroup's four waves and, for more
+// parallelism, over `ksplit` workgroups whose partials land ksplit * N floats
+// apart (summed in split order by the consumer).  The LM head (many rows)
+// gives each wave its own 16 rows over the whole K instead.  Loads are buffer
+// loads with clamped, branch-free addressing and run a stage of four tiles
+// ahead of the matrix work.
 #include "jev_dev.h"
 
 namespace jev {
 
 namespace {
 
-constexpr int kRowsPerWave = 4;
-constexpr int kWaves = 4;
-constexpr int kRowsPerBlock = kRowsPerWave * kWaves;
+constexpr int kDepth = 4; // tiles (block pairs) per pipeline stage
 
-template <int TYPE>
-struct Unit {
-    static constexpr int E = TYPE == kQ8_0 ? 16 : 32; // elements per lane-step
-    static constexpr int G = E / 4;                   // float4 groups
+// One lane's share of a tile: its quants for both blocks, the two scales /
+// mins of its row and its fifth bits.
+struct RawTile {
+    uint4 q;       // Q8_0: 16 bytes; Q4_0 / Q5_1: 8 bytes in .x, .y
+    uint32_t d, m; // two fp16 each (block 0 low half)
+    uint32_t qh;   // Q5_1: two bytes (block 0 low byte)
 };
 
-struct alignas(16) u32x4 {
-    uint32_t x, y, z, w;
-};
-
-// Dot of one unit of row r with the lane's x fragment.
+// B fragment of block bb of the tile: 8 fp16 integers for k = 8g .. 8g + 7.
 template <int TYPE>
-__device__ __forceinline__ float unit_dot(const QWeight &w, int r, int u, const float4 *xf, float xsum)
+__device__ __forceinline__ half8_t decode_frag(const RawTile &t, int bb)
 {
-    const int nb = w.cols >> 5;
+    uint32_t o0, o1, o2, o3;
     if (TYPE == kQ8_0) {
-        const u32x4 q = *(const u32x4 *)(w.qs + (size_t)r * w.cols + (size_t)u * 16);
-        float d = h2f(w.d[(size_t)r * nb + (u >> 1)]);
-        uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-        float p = 0.f;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            float4 xv = xf[g];
-            p = fmaf(xv.x, (float)(int8_t)(wd[g]), p);
-            p = fmaf(xv.y, (float)(int8_t)(wd[g] >> 8), p);
-            p = fmaf(xv.z, (float)(int8_t)(wd[g] >> 16), p);
-            p = fmaf(xv.w, (float)(int8_t)(wd[g] >> 24), p);
-        }
-        return d * p;
+        const uint32_t w0 = bb ? t.q.z : t.q.x, w1 = bb ? t.q.w : t.q.y;
+        bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
+        bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
     } else {
-        const u32x4 q = *(const u32x4 *)(w.qs + (size_t)r * (w.cols >> 1) + (size_t)u * 16);
-        size_t blk = (size_t)r * nb + u;
-        float d = h2f(w.d[blk]);
-        uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-        uint32_t qh = TYPE == kQ5_1 ? w.qh[blk] : 0u;
-        float p = 0.f;
-        // elements 0..15: low nibbles; 16..31: high nibbles.  xf[g] holds
-        // elements 4g..4g+3.
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            float4 xv = xf[g];
-            uint32_t word = wd[g & 3];
-            uint32_t nib = g < 4 ? (word & 0x0f0f0f0fu) : ((word >> 4) & 0x0f0f0f0fu);
-            if (TYPE == kQ5_1) {
-                // bits 4g..4g+3 of qh -> bit 4 of each byte
-                uint32_t hb = (qh >> (4 * g)) & 15u;
-                uint32_t spread = (hb * 0x00204081u) & 0x01010101u;
-                nib |= spread << 4;
-            }
-            float q0 = (float)(nib & 0xff), q1 = (float)((nib >> 8) & 0xff);
-            float q2 = (float)((nib >> 16) & 0xff), q3 = (float)(nib >> 24);
-            if (TYPE == kQ4_0) {
-                q0 -= 8.f;
-                q1 -= 8.f;
-                q2 -= 8.f;
-                q3 -= 8.f;
-            }
-            p = fmaf(xv.x, q0, p);
-            p = fmaf(xv.y, q1, p);
-            p = fmaf(xv.z, q2, p);
-            p = fmaf(xv.w, q3, p);
+        const uint32_t w = bb ? t.q.y : t.q.x;
+        uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
+        _Float16 bias = (_Float16)1032.0f;
+        if (TYPE == kQ5_1) {
+            const uint32_t hb = (t.qh >> (8 * bb)) & 0xffu;
+            n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
+            n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
+            bias = (_Float16)1024.0f;
         }
-        float r0 = d * p;
-        if (TYPE == kQ5_1) r0 = fmaf(h2f(w.m[blk]), xsum, r0);
-        return r0;
+        bytes_to_f16(n0, bias, o0, o1);
+        bytes_to_f16(n1, bias, o2, o3);
     }
+    return __builtin_bit_cast(half8_t, make_uint4(o0, o1, o2, o3));
 }
+
+__device__ __forceinline__ float half_of(uint32_t v, int hi) { return h2f((uint16_t)(hi ? v >> 16 : v)); }
+
+// Per-lane loader of one weight's 16-row group: scalar resources and
+// per-lane offsets fixed for the loop, a scalar offset per tile.
+template <int TYPE>
+struct TileLoader {
+    rsrc_t rq, rd, rm, rh;
+    uint32_t vq, vd, vh;
+    int tile0; // first tile of the row group
+
+    __device__ void init(const QWeight &w, int rg, int lane)
+    {
+        const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
+        const uint32_t tiles = (uint32_t)RG * KP;
+        rq = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
+        rd = make_rsrc(w.d, tiles * 64);
+        if (TYPE == kQ5_1) {
+            rm = make_rsrc(w.m, tiles * 64);
+            rh = make_rsrc(w.qh, tiles * 128);
+        }
+        vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8);
+        vd = 4 * (lane & 15);
+        vh = 2 * lane;
+        tile0 = min(rg, RG - 1) * KP; // groups past the weight feed unstored outputs
+    }
+
+    __device__ RawTile load(int kp) const
+    {
+        RawTile t;
+        const int tile = tile0 + kp;
+        if (TYPE == kQ8_0) {
+            t.q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, vq, tile * 1024, 0));
+        } else {
+            uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, vq, tile * 512, 0));
+            t.q = make_uint4(v.x, v.y, 0u, 0u);
+        }
+        t.d = __builtin_amdgcn_raw_buffer_load_b32(rd, vd, tile * 64, 0);
+        if (TYPE == kQ5_1) {
+            t.m = __builtin_amdgcn_raw_buffer_load_b32(rm, vd, tile * 64, 0);
+            t.qh = __builtin_amdgcn_raw_buffer_load_b16(rh, vh, tile * 128, 0);
+        }
+        return t;
+    }
+};
 
 } // namespace
 
-// LDS x layout: unit u = 64 c + l of lane l, group g, element i of the group
-// lives at ((c * G + g) * 64 + l) * 4 + i.
-template <int TYPE>
-__global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows_total)
+// WR: waves along rows (4: each wave its own 16 rows over the whole range;
+// 1: the four waves share 16 rows and split the range).  Grid: (row groups /
+// WR, ksplit).  nbz: quant blocks per K split (even).
+template <int TYPE, int WR, bool SWIGLU>
+__global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
 {
-    extern __shared__ float smem[];
-    constexpr int E = Unit<TYPE>::E, G = Unit<TYPE>::G;
-    const int K = a.K;
-    const int U = K / E;
-    const int chunks = (U + 63) / 64;
-    float *xs = smem;                       // chunks * G * 64 * 4 floats
-    float *bsum = smem + chunks * G * 256;  // Q5_1 block sums, U floats
-    for (int i = threadIdx.x; i < K; i += 256) {
-        int u = i / E, e = i % E;
-        int c = u >> 6, l = u & 63, g = e >> 2, k = e & 3;
-        xs[((c * G + g) * 64 + l) * 4 + k] = a.x[i];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int NW = SWIGLU ? 2 : 1; // weights per row (gate and up)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, rl = lane & 15;
+    const int nb = a.K >> 5;
+    const int z = blockIdx.y;
+    const int kb0 = z * nbz, nbw = min(nb - kb0, nbz); // this workgroup's blocks
+    const int ntw = (nbw + 1) >> 1;                     // ... and tiles (the odd last block pads)
+
+    // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
+    uint16_t *xh = (uint16_t *)smem, *xl = xh + nbz * 32, *zero = xl + nbz * 32;
+    float *xsum = (float *)(zero + 8);
+    float *red = xsum + nbz; // [4][NW][16] wave partials
+    for (int i = tid; i < 2 * ntw * 32; i += 256) {
+        uint16_t h = 0, l = 0;
+        if (i < nbw * 32) split_f16(a.x[(size_t)kb0 * 32 + i], h, l);
+        xh[i] = h;
+        xl[i] = l;
     }
+    if (tid < 8) zero[tid] = 0;
     if (TYPE == kQ5_1) {
         __syncthreads();
-        for (int u = threadIdx.x; u < U; u += 256) {
-            int c = u >> 6, l = u & 63;
+        for (int b = tid; b < 2 * ntw; b += 256) {
             float s = 0.f;
-            for (int g = 0; g < G; g++)
-                for (int k = 0; k < 4; k++) s += xs[((c * G + g) * 64 + l) * 4 + k];
-            bsum[u] = s;
+            for (int i = 0; i < 32; i++) s += h2f(xh[32 * b + i]) + h2f(xl[32 * b + i]);
+            xsum[b] = s;
         }
     }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = blockIdx.x * kRowsPerBlock + wave * kRowsPerWave;
-    for (int i = 0; i < kRowsPerWave; i++) {
-        int gr = row0 + i; // row over the concatenated outputs
-        if (gr >= nrows_total) break;
-        // resolve segment
-        int s = 0, r = gr;
-        if (!a.swiglu) {
-            while (s + 1 < a.nseg && r >= a.seg[s].rows) {
-                r -= a.seg[s].rows;
-                s++;
+    // ---- this wave's row group and tiles
+    const int rg = WR == 4 ? blockIdx.x * 4 + wave : blockIdx.x;
+    const int per = WR == 4 ? ntw : (ntw + 3) / 4;
+    const int t0 = WR == 4 ? 0 : min(ntw, wave * per);
+    const int ntiles = min(ntw, t0 + per) - t0;
+    const int kp0 = (kb0 >> 1) + t0; // first block pair (kb0 is even)
+
+    TileLoader<TYPE> ld[NW];
+    {
+        int g0 = rg, seg = 0;
+        if (!SWIGLU)
+            while (seg + 1 < a.nseg && g0 >= a.seg[seg].rows / 16) {
+                g0 -= a.seg[seg].rows / 16;
+                seg++;
             }
-        }
-        float acc = 0.f, acc2 = 0.f;
-        for (int c = 0; c < chunks; c++) {
-            int u = c * 64 + lane;
-            if (u >= U) break;
-            const float4 *xf = (const float4 *)(xs + (size_t)(c * G) * 256) + lane;
-            float4 xv[G];
+        seg = __builtin_amdgcn_readfirstlane(seg);
+        g0 = __builtin_amdgcn_readfirstlane(g0);
 #pragma unroll
-            for (int g = 0; g < G; g++) xv[g] = xf[g * 64];
-            float xsum = TYPE == kQ5_1 ? bsum[u] : 0.f;
-            acc += unit_dot<TYPE>(a.seg[s], r, u, xv, xsum);
-            if (a.swiglu) acc2 += unit_dot<TYPE>(a.seg[1], r, u, xv, xsum);
+        for (int w = 0; w < NW; w++) ld[w].init(a.seg[SWIGLU ? w : seg], g0, lane);
+    }
+    // A fragment address: row 0 -> hi, row 1 -> lo, rows 2..15 -> the zero slot
+    const uint16_t *abase = rl == 0 ? xh + 8 * g : rl == 1 ? xl + 8 * g : zero;
+    const int astep = rl <= 1 ? 32 : 0;
+
+    float acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) acc[w] = 0.f;
+
+    auto load_stage = [&](int st, RawTile (&r)[NW][kDepth]) {
+#pragma unroll
+        for (int j = 0; j < kDepth; j++) {
+            const int kp = kp0 + max(0, min(st * kDepth + j, ntiles - 1)); // clamped: reloads feed no output
+#pragma unroll
+            for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp);
         }
-        acc = warp_sum(acc);
-        if (a.swiglu) {
-            acc2 = warp_sum(acc2);
-            if (lane == 0) {
-                // Kernels.SwiGlu (Kernels.cs:82-89)
-                float gu = acc * acc2;
-                float e = expf(-acc);
-                float sg = 1.0f / (1.0f + e);
-                a.y[gr] = sg * gu;
+    };
+    auto compute_stage = [&](int st, const RawTile (&r)[NW][kDepth]) {
+#pragma unroll
+        for (int j = 0; j < kDepth; j++) {
+            const int tl = st * kDepth + j; // tile within the wave's range
+            const bool valid = tl < ntiles;
+            const int lt = t0 + min(tl, ntiles - 1); // tile within the workgroup's range
+#pragma unroll
+            for (int bb = 0; bb < 2; bb++) {
+                const half8_t af = *(const half8_t *)(abase + astep * (2 * lt + bb));
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    const half8_t bf = decode_frag<TYPE>(r[w][j], bb);
+                    floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const float dv = valid ? half_of(r[w][j].d, bb) : 0.f;
+                    const float v = p[0] + p[1];
+                    acc[w] = fmaf(dv, v, acc[w]);
+                    if (TYPE == kQ5_1) {
+                        const float mv = valid ? half_of(r[w][j].m, bb) : 0.f;
+                        acc[w] = fmaf(mv, xsum[2 * lt + bb], acc[w]);
+                    }
+                }
             }
-        } else if (lane == 0) {
-            a.y[gr] = acc;
+        }
+    };
+
+    // Two register stages; whole pairs in the loop, the odd stage after it.
+    const int nst = (ntiles + kDepth - 1) / kDepth;
+    RawTile r0[NW][kDepth], r1[NW][kDepth];
+    if (nst > 0) {
+        load_stage(0, r0);
+        int st = 0;
+        for (; st + 2 <= nst; st += 2) {
+            load_stage(st + 1, r1);
+            compute_stage(st, r0);
+            load_stage(st + 2, r0);
+            compute_stage(st + 1, r1);
+        }
+        if (st < nst) compute_stage(st, r0);
+    }
+
+    // ---- outputs: lane l < 16 holds row rg * 16 + l
+    const int row = rg * 16 + rl;
+    if (WR == 4) {
+        if (g == 0 && row < nrows) a.y[(size_t)z * nrows + row] = acc[0];
+    } else {
+        if (g == 0) {
+#pragma unroll
+            for (int w = 0; w < NW; w++) red[(wave * NW + w) * 16 + rl] = acc[w];
+        }
+        __syncthreads();
+        if (wave == 0 && g == 0 && row < nrows) {
+            float s[NW];
+#pragma unroll
+            for (int w = 0; w < NW; w++)
+                s[w] = ((red[(0 * NW + w) * 16 + rl] + red[(1 * NW + w) * 16 + rl]) + red[(2 * NW + w) * 16 + rl]) +
+                       red[(3 * NW + w) * 16 + rl];
+            if (SWIGLU) {
+                // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g)
+                float gu = s[0] * s[NW - 1];
+                float e = expf(-s[0]);
+                float sg = 1.0f / (1.0f + e);
+                a.y[row] = sg * gu;
+            } else {
+                a.y[(size_t)z * nrows + row] = s[0];
+            }
         }
     }
+}
+
+template <int TYPE, int WR, bool SWIGLU>
+static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
+{
+    const int nb = a.K >> 5;
+    const int nbz = gemm_split_blocks(nb, a.ksplit);
+    const int groups = (rows + 15) / 16;
+    size_t lds = (size_t)nbz * 32 * 2 * 2 + 16 + (size_t)nbz * 4 + 4 * 2 * 16 * 4; // nbz is even
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    dim3 grid(WR == 4 ? (groups + 3) / 4 : groups, a.ksplit);
+    hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU>), grid, dim3(256), lds, s, a, rows, nbz);
+    return hipGetLastError();
 }
 
 template <int TYPE>
 static hipError_t launch_gemv_typed(const GemvArgs &a, hipStream_t s)
 {
-    constexpr int E = Unit<TYPE>::E, G = Unit<TYPE>::G;
-    int U = a.K / E;
-    int chunks = (U + 63) / 64;
-    size_t lds = sizeof(float) * ((size_t)chunks * G * 256 + (TYPE == kQ5_1 ? U : 0));
-    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    if (a.swiglu) return launch_gemv_cfg<TYPE, 1, true>(a, a.seg[0].rows, s);
     int rows = 0;
-    if (a.swiglu) rows = a.seg[0].rows;
-    else
-        for (int i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
-    int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipLaunchKernelGGL(gemv_q_kernel<TYPE>, dim3(blocks), dim3(256), lds, s, a, rows);
-    return hipGetLastError();
+    for (int i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
+    if (gemv_rows_mode(rows)) return launch_gemv_cfg<TYPE, 4, false>(a, rows, s);
+    return launch_gemv_cfg<TYPE, 1, false>(a, rows, s);
 }
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s)
 {
-    if (a.K % 32 != 0) return hipErrorInvalidValue;
-    for (int i = 0; i < a.nseg; i++)
+    if (a.K % 32 != 0 || a.K <= 0 || a.ksplit < 1) return hipErrorInvalidValue;
+    const int nb = a.K >> 5;
+    if (a.ksplit > 1 && (a.swiglu || gemm_split_blocks(nb, a.ksplit) * (a.ksplit - 1) >= nb)) return hipErrorInvalidValue;
+    for (int i = 0; i < a.nseg; i++) {
         if (a.seg[i].type != a.seg[0].type || a.seg[i].cols != a.K) return hipErrorInvalidValue;
+        // a 16-row group (tile row) never straddles two segments
+        if (!a.swiglu && i + 1 < a.nseg && a.seg[i].rows % 16 != 0) return hipErrorInvalidValue;
+    }
     if (a.swiglu && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows)) return hipErrorInvalidValue;
     switch (a.seg[0].type) {
     case kQ8_0: return launch_gemv_typed<kQ8_0>(a, s);

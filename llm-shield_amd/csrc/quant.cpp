@@ -101,15 +101,14 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 QLayout qlayout(int type, int64_t rows, int64_t cols)
 {
     QLayout l{0, 0, 0, 0, 0};
-    size_t nb = (size_t)(cols / 32) * (size_t)rows;
-    size_t qs = type == kQ8_0 ? (size_t)rows * cols : (size_t)rows * cols / 2;
+    const size_t tiles = (size_t)tile_rows((int)rows) * (size_t)tile_kpairs((int)cols);
     l.qs = 0;
-    l.d = align256(qs);
-    size_t end = l.d + nb * 2;
+    l.d = align256(tiles * tile_qs_bytes(type));
+    size_t end = l.d + tiles * 64;
     if (type == kQ5_1) {
         l.m = align256(end);
-        l.qh = align256(l.m + nb * 2);
-        end = l.qh + nb * 4;
+        l.qh = align256(l.m + tiles * 64);
+        end = l.qh + tiles * 128;
     }
     l.total = align256(end);
     return l;
@@ -117,6 +116,8 @@ QLayout qlayout(int type, int64_t rows, int64_t cols)
 
 static void parallel_rows(int64_t rows, int threads, const std::function<void(int64_t, int64_t)> &fn);
 
+// GGUF blocks -> tiles.  Element (r, k) of a block pair goes to lane
+// l = 16 (k % 32 / 8) + r % 16; see the layout description in jev_internal.h.
 bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *dst, int threads)
 {
     if ((type != kQ8_0 && type != kQ4_0 && type != kQ5_1) || cols % 32 != 0 || rows <= 0) return false;
@@ -124,21 +125,46 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
     const uint8_t *src = (const uint8_t *)gguf;
     uint8_t *out = (uint8_t *)dst;
     const int64_t nb = cols / 32, ts = type_size(type);
+    const int64_t KP = tile_kpairs((int)cols), RG = tile_rows((int)rows);
+    const size_t TQ = tile_qs_bytes(type);
+    // zero padding (rows past the weight, the odd last block) and alignment gaps
+    parallel_rows(RG, threads, [&](int64_t g0, int64_t g1) {
+        auto clear = [&](size_t off, size_t per_tile) { std::memset(out + off + g0 * KP * per_tile, 0, (g1 - g0) * KP * per_tile); };
+        clear(L.qs, TQ);
+        clear(L.d, 64);
+        if (type == kQ5_1) {
+            clear(L.m, 64);
+            clear(L.qh, 128);
+        }
+    });
     parallel_rows(rows, threads, [&](int64_t r0, int64_t r1) {
-        for (int64_t r = r0; r < r1; r++) {
-            const uint8_t *row = src + r * nb * ts;
+        for (int64_t row = r0; row < r1; row++) {
+            const uint8_t *rowp = src + row * nb * ts;
+            const int64_t rg = row / 16, r = row % 16;
             for (int64_t b = 0; b < nb; b++) {
-                const uint8_t *blk = row + b * ts;
-                size_t bi = (size_t)r * nb + b;
-                std::memcpy(out + L.d + 2 * bi, blk, 2);
+                const uint8_t *blk = rowp + b * ts;
+                const size_t tile = (size_t)(rg * KP + b / 2);
+                const int bb = (int)(b & 1);
+                std::memcpy(out + L.d + tile * 64 + 4 * r + 2 * bb, blk, 2);
                 if (type == kQ8_0) {
-                    std::memcpy(out + L.qs + (size_t)r * cols + 32 * b, blk + 2, 32);
-                } else if (type == kQ4_0) {
-                    std::memcpy(out + L.qs + (size_t)r * cols / 2 + 16 * b, blk + 2, 16);
-                } else {
-                    std::memcpy(out + L.m + 2 * bi, blk + 2, 2);
-                    std::memcpy(out + L.qh + 4 * bi, blk + 4, 4);
-                    std::memcpy(out + L.qs + (size_t)r * cols / 2 + 16 * b, blk + 8, 16);
+                    for (int g = 0; g < 4; g++)
+                        std::memcpy(out + L.qs + tile * TQ + 16 * (16 * g + r) + 8 * bb, blk + 2 + 8 * g, 8);
+                    continue;
+                }
+                // element j of the block: low nibble of byte j (j < 16), high nibble of byte j - 16
+                const uint8_t *qs = blk + (type == kQ4_0 ? 2 : 8);
+                uint32_t qh = 0;
+                if (type == kQ5_1) {
+                    std::memcpy(out + L.m + tile * 64 + 4 * r + 2 * bb, blk + 2, 2);
+                    std::memcpy(&qh, blk + 4, 4);
+                }
+                for (int g = 0; g < 4; g++) {
+                    uint8_t *dq = out + L.qs + tile * TQ + 8 * (16 * g + r) + 4 * bb;
+                    for (int i = 0; i < 4; i++) {
+                        auto nib = [&](int j) { return j < 16 ? (qs[j] & 15) : (qs[j - 16] >> 4); };
+                        dq[i] = (uint8_t)(nib(8 * g + i) | (nib(8 * g + i + 4) << 4));
+                    }
+                    if (type == kQ5_1) out[L.qh + tile * 128 + 2 * (16 * g + r) + bb] = (uint8_t)((qh >> (8 * g)) & 0xffu);
                 }
             }
         }

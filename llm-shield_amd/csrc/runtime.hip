@@ -142,11 +142,13 @@ struct jev_ctx {
     int qdim() const { return cfg.n_heads * cfg.head_dim; }
     int kvdim() const { return cfg.n_kv_heads * cfg.head_dim; }
     const QWeight &table() const { return output.base ? output : embd; }
-    // K-split counts of the store-mode projections (GEMM path, two or more
-    // tokens); partials are summed by the kernel that consumes the output.
-    int split_qkv() const { return gemm_choose_split(qdim() + 2 * kvdim(), cfg.hidden); }
-    int split_o() const { return gemm_choose_split(cfg.hidden, qdim()); }
-    int split_down() const { return gemm_choose_split(cfg.hidden, cfg.ffn); }
+    // K-split counts of the store-mode projections for a call of T tokens
+    // (GEMM for two or more, GEMV for one); the partials are summed by the
+    // kernel that consumes the output.
+    static int split(int T, int N, int K) { return T >= 2 ? gemm_choose_split(N, K) : gemv_choose_split(N, K); }
+    int split_qkv(int T) const { return split(T, qdim() + 2 * kvdim(), cfg.hidden); }
+    int split_o(int T) const { return split(T, cfg.hidden, qdim()); }
+    int split_down(int T) const { return split(T, cfg.hidden, cfg.ffn); }
     size_t layer_stride() const { return (size_t)cfg.n_kv_heads * cap * cfg.head_dim; }
 };
 
@@ -254,7 +256,7 @@ int upload_weight(int type, int64_t rows, int64_t cols, const void *bytes, QWeig
     w.qs = b8 + L.qs;
     w.d = (const uint16_t *)(b8 + L.d);
     w.m = type == kQ5_1 ? (const uint16_t *)(b8 + L.m) : nullptr;
-    w.qh = type == kQ5_1 ? (const uint32_t *)(b8 + L.qh) : nullptr;
+    w.qh = type == kQ5_1 ? b8 + L.qh : nullptr;
     return JEV_OK;
 }
 
@@ -312,9 +314,9 @@ int kv_ensure(jev_ctx *c, int required)
 
 bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a.type == b.type && b.type == c.type; }
 
-// One linear step y = x . W^T over up to three weights sharing x.  T >= 2:
-// MFMA GEMM on the fp16 pair, as `ksplit` K-split partials T * ldy floats
-// apart; T == 1: GEMV on fp32 x (one partial).
+// One linear step y = x . W^T over up to three weights sharing x, as
+// `ksplit` K-split partials T * ldy floats apart.  T >= 2: MFMA GEMM on the
+// fp16 pair in the operand-tile layout; T == 1: GEMV on fp32 x.
 int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xt, const float *xsum,
            const float *x32, float *y, int ldy, int ksplit)
 {
@@ -331,6 +333,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
         g.nseg = nw;
         for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
         g.y = y;
+        g.ksplit = ksplit;
         ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows));
         HIP_TRY(launch_gemv(g, c->stream));
         return JEV_OK;
@@ -356,10 +359,9 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
     size_t qkv = (size_t)c->qdim() + 2 * c->kvdim();
     size_t wide = std::max<size_t>({(size_t)f.hidden, (size_t)c->qdim(), (size_t)f.ffn});
     HIP_TRY(c->h.ensure((size_t)T * f.hidden));
-    const bool multi = T >= 2;
-    HIP_TRY(c->y.ensure((size_t)T * qkv * (multi ? c->split_qkv() : 1)));
-    HIP_TRY(c->yo.ensure((size_t)T * f.hidden * (multi ? c->split_o() : 1)));
-    HIP_TRY(c->ydown.ensure((size_t)T * f.hidden * (multi ? c->split_down() : 1)));
+    HIP_TRY(c->y.ensure((size_t)T * qkv * c->split_qkv(T)));
+    HIP_TRY(c->yo.ensure((size_t)T * f.hidden * c->split_o(T)));
+    HIP_TRY(c->ydown.ensure((size_t)T * f.hidden * c->split_down(T)));
     HIP_TRY(c->q.ensure((size_t)T * c->qdim()));
     HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + 1));
     if (T == 1) {
@@ -539,7 +541,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     (void)q51;
     hipStream_t s = c->stream;
 
-    const int s_o = T >= 2 ? c->split_o() : 1, s_down = T >= 2 ? c->split_down() : 1;
+    const int s_o = c->split_o(T), s_down = c->split_down(T);
     const size_t stride_d = (size_t)T * D; // floats between partials of yo / ydown
     HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
     for (int l = 0; l < f.n_layers; l++) {
@@ -569,7 +571,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         const int ldqkv = qdim + 2 * kvdim;
         bool fuse = same_type3(L.q, L.k, L.v) && (T == 1 || (qdim % 128 == 0 && kvdim % 128 == 0));
         // separate projections share y's columns, so they are not split
-        const int s_qkv = T >= 2 && fuse ? c->split_qkv() : 1;
+        const int s_qkv = fuse ? c->split_qkv(T) : 1;
         if (fuse) {
             const QWeight *ws[3] = {&L.q, &L.k, &L.v};
             int rc = linear(c, T, ws, 3, c->xt.p, c->xsum.p, c->x32.p, c->y.p, ldqkv, s_qkv);
@@ -1270,7 +1272,7 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
     float *dx = nullptr, *dy = nullptr, *dsum = nullptr;
     uint16_t *xt = nullptr;
     hipError_t e = hipMalloc((void **)&dx, nx * sizeof(float));
-    const int ksplit = tokens >= 2 ? gemm_choose_split((int)rows, (int)cols) : 1;
+    const int ksplit = jev_ctx::split(tokens, (int)rows, (int)cols);
     if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * ksplit * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess && tokens >= 2) {
@@ -1298,7 +1300,9 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
         g.x = dx;
         g.seg[0] = w;
         g.y = dy;
+        g.ksplit = ksplit;
         e = launch_gemv(g, nullptr);
+        if (e == hipSuccess && ksplit > 1) e = launch_reduce_partials(dy, ksplit, 1, (int)rows, dy, nullptr);
     }
     if (e == hipSuccess) e = hipMemcpy(y, dy, ny * sizeof(float), hipMemcpyDeviceToHost);
     for (void *pp : {(void *)dx, (void *)dy, (void *)dsum, (void *)xt})
