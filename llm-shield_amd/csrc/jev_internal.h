@@ -173,6 +173,7 @@ struct RopeArgs {
     int cap = 0;
     const int32_t *pos = nullptr, *slot = nullptr;
     int start = 0; // used when pos/slot are null (causal append)
+    const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     const float *freqs = nullptr;
     float mscale = 1.f;
     int orig_ctx = 0;
@@ -205,8 +206,10 @@ struct DecodeAttnArgs {
     int cap = 0;
     const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
     int start = 0; // causal append when the arrays are null
+    const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     float scale = 0.f;
-    float *part = nullptr; // [T][heads][max_chunks][hd + 2]
+    float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
+    int *counters = nullptr; // [T][n_heads / group], zero between calls
     float *ctx = nullptr;
 };
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
@@ -222,6 +225,11 @@ struct HeadRowsArgs {
 hipError_t launch_head_rows(const HeadRowsArgs &a, hipStream_t s);
 
 // Lowest index of the maximum of x[0..n).
+// Greedy decode step: the argmax of x (ties to the lower index) becomes the
+// next token: state[2] = token, out[state[1]] = token, then the step
+// (state[1]) and the cache length (state[0]) advance by one.
+hipError_t launch_argmax_decode(const float *x, int n, float *sv, int32_t *si, int32_t *state, int32_t *out,
+                                hipStream_t s);
 hipError_t launch_argmax(const float *x, int n, int32_t *result, float *scratch_val, int32_t *scratch_idx,
                          hipStream_t s);
 

@@ -28,9 +28,9 @@
 //   O^T (128 x 16) += V^T (128 x 64) . P^T (64 x 16)      48 MFMAs per 64 keys,
 //                     keys taken in the order the S^T fragments hold them
 //
-// Decode kernel (attn_decode_kernel): one query per token, split over chunks
-// of 64 logical keys (one wave each: lane = key for the scores, lane = two
-// dims for the weighted sum), chunks combined in ascending order.
+// Decode kernel (attn_decode_kernel): few tokens, one query per head, split
+// over chunks of 64 logical keys per KV head; chunks combined in ascending
+// order by the last workgroup to finish.
 #include "jev_dev.h"
 
 namespace jev {
@@ -108,16 +108,20 @@ __global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
         // Stage K: thread -> (key, quarter row) as pairs in [key][dim].
         {
             int key = tid >> 2, part = tid & 3;
-            int kl = b * KB + key;
+            const bool ok = b * KB + key < max_limit;
+            const int kl = min(b * KB + key, max_limit - 1);
             uint2 hv[8], lv[8];
-            if (kl < max_limit) {
-                int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
+            {
+                const int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
                 const float4 *ks = (const float4 *)(kbase + (size_t)p * 128 + part * 32);
+                float4 kr[8];
 #pragma unroll
-                for (int i = 0; i < 8; i++) split4(ks[i], hv[i], lv[i]);
-            } else {
+                for (int i = 0; i < 8; i++) kr[i] = ks[i];
 #pragma unroll
-                for (int i = 0; i < 8; i++) hv[i] = lv[i] = make_uint2(0u, 0u);
+                for (int i = 0; i < 8; i++) {
+                    split4(kr[i], hv[i], lv[i]);
+                    if (!ok) hv[i] = lv[i] = make_uint2(0u, 0u);
+                }
             }
             uint4 *kh4 = (uint4 *)(Kh + key * KROW + part * 32);
             uint4 *kl4 = (uint4 *)(Kl + key * KROW + part * 32);
@@ -128,22 +132,25 @@ __global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
             }
         }
         // Stage V transposed: thread -> 4 keys x 8 dims, written as [dim][key].
+        // Loads are unconditional (clamped key, value zeroed past the end) so
+        // all four keys' rows are in flight together.
         {
             int kg = tid >> 4, dg = tid & 15;
             float vv[4][8];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                int kl = b * KB + 4 * kg + kk;
-                if (kl < max_limit) {
-                    int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
-                    const float4 *vs = (const float4 *)(vbase + (size_t)p * 128 + 8 * dg);
-                    float4 v0 = vs[0], v1 = vs[1];
-                    vv[kk][0] = v0.x; vv[kk][1] = v0.y; vv[kk][2] = v0.z; vv[kk][3] = v0.w;
-                    vv[kk][4] = v1.x; vv[kk][5] = v1.y; vv[kk][6] = v1.z; vv[kk][7] = v1.w;
-                } else {
+                const int kl = min(b * KB + 4 * kg + kk, max_limit - 1);
+                const int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
+                const float4 *vs = (const float4 *)(vbase + (size_t)p * 128 + 8 * dg);
+                const float4 v0 = vs[0], v1 = vs[1];
+                vv[kk][0] = v0.x; vv[kk][1] = v0.y; vv[kk][2] = v0.z; vv[kk][3] = v0.w;
+                vv[kk][4] = v1.x; vv[kk][5] = v1.y; vv[kk][6] = v1.z; vv[kk][7] = v1.w;
+            }
 #pragma unroll
-                    for (int i = 0; i < 8; i++) vv[kk][i] = 0.f;
-                }
+            for (int kk = 0; kk < 4; kk++) {
+                const bool ok = b * KB + 4 * kg + kk < max_limit;
+#pragma unroll
+                for (int i = 0; i < 8; i++) vv[kk][i] = ok ? vv[kk][i] : 0.f;
             }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -250,98 +257,169 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 
 // ------------------------------------------------------------ decode
 
-__global__ __launch_bounds__(64) void attn_decode_kernel(DecodeAttnArgs a)
+// One workgroup per (token, KV head, chunk of 64 logical keys): the chunk's K
+// and V rows are staged in LDS once with coalesced loads and serve the
+// group's query heads (wave w takes heads w, w + 4, ...).  Scores: lane =
+// key, fp32 dot over 128 dims; weighted sum: lane = two dims.  Each chunk
+// leaves (max, sum, o[128]) per head; the last workgroup of a (token, KV
+// head) to finish -- counted with an atomic that it resets -- combines the
+// chunks in ascending order, so the result does not depend on timing.
+constexpr int kDecKeys = 64;
+constexpr int kDecRow = 132; // padded K row, floats
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 {
-    __shared__ float qs[128];
-    __shared__ float ps[64];
-    const int t = blockIdx.x, head = blockIdx.y, c = blockIdx.z;
-    const int lane = threadIdx.x;
-    const int kvh = head / a.group;
+    __shared__ __attribute__((aligned(16))) float Ks[kDecKeys * kDecRow];
+    __shared__ __attribute__((aligned(16))) float Vs[kDecKeys * 128];
+    __shared__ __attribute__((aligned(16))) float qs[4][128];
+    __shared__ float ps[4][kDecKeys];
+    __shared__ int last;
+    const int t = blockIdx.x, kvh = blockIdx.y, c = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qdim = a.n_heads * 128;
-    const int slot = a.slot ? a.slot[t] : a.start + t;
+    const int start = a.start_dev ? *a.start_dev : a.start;
+    const int slot = a.slot ? a.slot[t] : start + t;
     const int slo = a.shared_lo ? a.shared_lo[t] : 0;
-    const int shi = a.shared_hi ? a.shared_hi[t] : a.start;
-    const int seg = a.segment ? a.segment[t] : a.start;
+    const int shi = a.shared_hi ? a.shared_hi[t] : start;
+    const int seg = a.segment ? a.segment[t] : start;
     const int n_sh = shi - slo;
     const int limit = n_sh + (slot - seg + 1);
-    float *part = a.part + (((size_t)t * a.n_heads + head) * a.max_chunks + c) * 130;
+    const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
+    if (c >= nchunks) return; // this token sees fewer keys
 
-    if (c * 64 >= limit) {
-        if (lane == 0) {
-            part[0] = -INFINITY;
-            part[1] = 0.f;
-        }
-        for (int d = lane; d < 128; d += 64) part[2 + d] = 0.f;
-        return;
-    }
-    const float *q = a.q + (size_t)t * qdim + head * 128;
-    qs[lane] = q[lane];
-    qs[lane + 64] = q[lane + 64];
-    __syncthreads();
-
+    // ---- stage the chunk's K and V rows (logical key -> cache slot)
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
-    int kl = c * 64 + lane;
-    float sc = -INFINITY;
-    if (kl < limit) {
-        int p = kl < n_sh ? slo + kl : seg + (kl - n_sh);
-        const float4 *kr = (const float4 *)(kbase + (size_t)p * 128);
-        float acc = 0.f;
-#pragma unroll 8
-        for (int i = 0; i < 32; i++) {
-            float4 kv = kr[i];
-            acc = fmaf(qs[4 * i], kv.x, acc);
-            acc = fmaf(qs[4 * i + 1], kv.y, acc);
-            acc = fmaf(qs[4 * i + 2], kv.z, acc);
-            acc = fmaf(qs[4 * i + 3], kv.w, acc);
+    const int nk = min(kDecKeys, limit - c * kDecKeys);
+    {
+        // unconditional (clamped) loads, all in flight before the first store
+        float4 kv[8], vv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int e = tid + 256 * i; // float4 index in the 64 x 32 chunk
+            const int key = min(e >> 5, nk - 1), d4 = e & 31;
+            const int kl = c * kDecKeys + key;
+            const int p = kl < n_sh ? slo + kl : seg + (kl - n_sh);
+            kv[i] = *(const float4 *)(kbase + (size_t)p * 128 + 4 * d4);
+            vv[i] = *(const float4 *)(vbase + (size_t)p * 128 + 4 * d4);
         }
-        sc = acc * a.scale;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int e = tid + 256 * i;
+            const int key = e >> 5, d4 = e & 31;
+            const bool ok = key < nk;
+            const float4 k4 = kv[i], v4 = vv[i];
+            *(float4 *)(Ks + key * kDecRow + 4 * d4) =
+                make_float4(ok ? k4.x : 0.f, ok ? k4.y : 0.f, ok ? k4.z : 0.f, ok ? k4.w : 0.f);
+            *(float4 *)(Vs + key * 128 + 4 * d4) =
+                make_float4(ok ? v4.x : 0.f, ok ? v4.y : 0.f, ok ? v4.z : 0.f, ok ? v4.w : 0.f);
+        }
     }
-    float mx = warp_max(sc);
-    float p = kl < limit ? expf(sc - mx) : 0.f;
-    float sum = warp_sum(p);
-    ps[lane] = p;
-    __syncthreads();
-    float o0 = 0.f, o1 = 0.f;
-    int nk = min(64, limit - c * 64);
-    for (int k = 0; k < nk; k++) {
-        int kk = c * 64 + k;
-        int pp = kk < n_sh ? slo + kk : seg + (kk - n_sh);
-        float2 vv = *(const float2 *)(vbase + (size_t)pp * 128 + 2 * lane);
-        float w = ps[k];
-        o0 = fmaf(w, vv.x, o0);
-        o1 = fmaf(w, vv.y, o1);
+    float *part_base = a.part + ((size_t)t * a.n_heads) * a.max_chunks * 130;
+    for (int h0 = 0; h0 < a.group; h0 += 4) { // every wave takes every barrier
+        const int h = h0 + wave;
+        const bool active = h < a.group;
+        const int head = kvh * a.group + min(h, a.group - 1);
+        __syncthreads(); // K/V staged; the previous head's qs/ps consumed
+        const float *q = a.q + (size_t)t * qdim + head * 128;
+        qs[wave][lane] = q[lane];
+        qs[wave][lane + 64] = q[lane + 64];
+        __syncthreads();
+        // scores: lane = key
+        float sc = -INFINITY;
+        if (lane < nk) {
+            float acc = 0.f;
+            const float4 *kr = (const float4 *)(Ks + lane * kDecRow);
+            const float4 *qr = (const float4 *)qs[wave];
+#pragma unroll 8
+            for (int i = 0; i < 32; i++) {
+                const float4 kv = kr[i], qv = qr[i];
+                acc = fmaf(qv.x, kv.x, acc);
+                acc = fmaf(qv.y, kv.y, acc);
+                acc = fmaf(qv.z, kv.z, acc);
+                acc = fmaf(qv.w, kv.w, acc);
+            }
+            sc = acc * a.scale;
+        }
+        const float mx = warp_max(sc);
+        const float p = lane < nk ? expf(sc - mx) : 0.f;
+        const float sum = warp_sum(p);
+        ps[wave][lane] = p;
+        __syncthreads();
+        // weighted sum: lane = dims 2 lane, 2 lane + 1
+        float o0 = 0.f, o1 = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < nk; k++) {
+            const float w = ps[wave][k];
+            const float2 vv = *(const float2 *)(Vs + k * 128 + 2 * lane);
+            o0 = fmaf(w, vv.x, o0);
+            o1 = fmaf(w, vv.y, o1);
+        }
+        if (active) {
+            float *part = part_base + ((size_t)head * a.max_chunks + c) * 130;
+            if (lane == 0) {
+                part[0] = mx;
+                part[1] = sum;
+            }
+            *(float2 *)(part + 2 + 2 * lane) = make_float2(o0, o1);
+        }
     }
-    if (lane == 0) {
-        part[0] = mx;
-        part[1] = sum;
-    }
-    part[2 + 2 * lane] = o0;
-    part[3 + 2 * lane] = o1;
-}
 
-__global__ __launch_bounds__(128) void attn_combine_kernel(DecodeAttnArgs a)
-{
-    const int t = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
-    const float *part = a.part + ((size_t)t * a.n_heads + head) * a.max_chunks * 130;
-    float M = -INFINITY;
-    for (int c = 0; c < a.max_chunks; c++) M = fmaxf(M, part[c * 130]);
-    float L = 0.f, O = 0.f;
-    for (int c = 0; c < a.max_chunks; c++) {
-        float mc = part[c * 130];
-        float f = mc == -INFINITY ? 0.f : expf(mc - M);
-        L = fmaf(part[c * 130 + 1], f, L);
-        O = fmaf(part[c * 130 + 2 + d], f, O);
+    // ---- the last chunk of this (token, KV head) to finish combines
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        int *ctr = a.counters + (size_t)t * (a.n_heads / a.group) + kvh;
+        const int done = atomicAdd(ctr, 1);
+        last = done == nchunks - 1;
+        if (last) *ctr = 0; // ready for the next call
     }
-    a.ctx[(size_t)t * a.n_heads * 128 + head * 128 + d] = O / L;
+    __syncthreads();
+    if (!last) return;
+    __threadfence(); // acquire: the other chunks' partials are visible
+    for (int h = wave; h < a.group; h += 4) {
+        const int head = kvh * a.group + h;
+        const float *part = part_base + (size_t)head * a.max_chunks * 130;
+        // chunks in ascending order, eight loads in flight at a time
+        float M = -INFINITY;
+        for (int c0 = 0; c0 < nchunks; c0 += 8) {
+            float mv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) mv[j] = part[min(c0 + j, nchunks - 1) * 130];
+#pragma unroll
+            for (int j = 0; j < 8; j++) M = fmaxf(M, mv[j]);
+        }
+        float L = 0.f, O0 = 0.f, O1 = 0.f;
+        for (int c0 = 0; c0 < nchunks; c0 += 8) {
+            float mv[8], lv[8];
+            float2 ov[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float *pc = part + min(c0 + j, nchunks - 1) * 130;
+                mv[j] = pc[0];
+                lv[j] = pc[1];
+                ov[j] = *(const float2 *)(pc + 2 + 2 * lane);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (c0 + j < nchunks) {
+                    const float f = expf(mv[j] - M);
+                    L = fmaf(lv[j], f, L);
+                    O0 = fmaf(ov[j].x, f, O0);
+                    O1 = fmaf(ov[j].y, f, O1);
+                }
+            }
+        }
+        float *ctx = a.ctx + (size_t)t * qdim + head * 128;
+        *(float2 *)(ctx + 2 * lane) = make_float2(O0 / L, O1 / L);
+    }
 }
 
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.hd != 128) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads, a.max_chunks), dim3(64), 0, s, a);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.T, a.n_heads), dim3(128), 0, s, a);
+    if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0 || !a.counters) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

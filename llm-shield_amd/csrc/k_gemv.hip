@@ -127,27 +127,6 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
     const int kb0 = z * nbz, nbw = min(nb - kb0, nbz); // this workgroup's blocks
     const int ntw = (nbw + 1) >> 1;                     // ... and tiles (the odd last block pads)
 
-    // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
-    uint16_t *xh = (uint16_t *)smem, *xl = xh + nbz * 32, *zero = xl + nbz * 32;
-    float *xsum = (float *)(zero + 8);
-    float *red = xsum + nbz; // [4][NW][16] wave partials
-    for (int i = tid; i < 2 * ntw * 32; i += 256) {
-        uint16_t h = 0, l = 0;
-        if (i < nbw * 32) split_f16(a.x[(size_t)kb0 * 32 + i], h, l);
-        xh[i] = h;
-        xl[i] = l;
-    }
-    if (tid < 8) zero[tid] = 0;
-    if (TYPE == kQ5_1) {
-        __syncthreads();
-        for (int b = tid; b < 2 * ntw; b += 256) {
-            float s = 0.f;
-            for (int i = 0; i < 32; i++) s += h2f(xh[32 * b + i]) + h2f(xl[32 * b + i]);
-            xsum[b] = s;
-        }
-    }
-    __syncthreads();
-
     // ---- this wave's row group and tiles
     const int rg = WR == 4 ? blockIdx.x * 4 + wave : blockIdx.x;
     const int per = WR == 4 ? ntw : (ntw + 3) / 4;
@@ -168,14 +147,6 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
 #pragma unroll
         for (int w = 0; w < NW; w++) ld[w].init(a.seg[SWIGLU ? w : seg], g0, lane);
     }
-    // A fragment address: row 0 -> hi, row 1 -> lo, rows 2..15 -> the zero slot
-    const uint16_t *abase = rl == 0 ? xh + 8 * g : rl == 1 ? xl + 8 * g : zero;
-    const int astep = rl <= 1 ? 32 : 0;
-
-    float acc[NW];
-#pragma unroll
-    for (int w = 0; w < NW; w++) acc[w] = 0.f;
-
     auto load_stage = [&](int st, RawTile (&r)[NW][kDepth]) {
 #pragma unroll
         for (int j = 0; j < kDepth; j++) {
@@ -184,6 +155,57 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
             for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp);
         }
     };
+    // the first stage's weights are in flight while x is staged
+    const int nst = (ntiles + kDepth - 1) / kDepth;
+    RawTile r0[NW][kDepth], r1[NW][kDepth];
+    if (nst > 0) load_stage(0, r0);
+
+    // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
+    uint16_t *xh = (uint16_t *)smem, *xl = xh + nbz * 32, *zero = xl + nbz * 32;
+    float *xsum = (float *)(zero + 8);
+    float *red = xsum + nbz; // [4][NW][16] wave partials
+    // thread -> 8 consecutive elements; a block's four groups are neighbouring lanes
+    for (int i0 = 0; i0 < 2 * ntw * 4; i0 += 256) {
+        const int i = i0 + tid;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (i < nbw * 4) {
+            const float4 *xp = (const float4 *)(a.x + (size_t)kb0 * 32 + 8 * i);
+            const float4 v0 = xp[0], v1 = xp[1];
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        }
+        uint32_t hw[4], lw[4];
+        float bs = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            uint16_t h0, l0, h1, l1;
+            split_f16(v[j], h0, l0);
+            split_f16(v[j + 1], h1, l1);
+            hw[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            lw[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            bs += (h2f(h0) + h2f(l0)) + (h2f(h1) + h2f(l1));
+        }
+        if (i < 2 * ntw * 4) {
+            *(uint4 *)(xh + 8 * i) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            *(uint4 *)(xl + 8 * i) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+        if (TYPE == kQ5_1) {
+            bs = bs + __shfl_xor(bs, 1, 64);
+            bs = bs + __shfl_xor(bs, 2, 64);
+            if (i < 2 * ntw * 4 && (i & 3) == 0) xsum[i >> 2] = bs;
+        }
+    }
+    if (tid < 8) zero[tid] = 0;
+    __syncthreads();
+
+    // A fragment address: row 0 -> hi, row 1 -> lo, rows 2..15 -> the zero slot
+    const uint16_t *abase = rl == 0 ? xh + 8 * g : rl == 1 ? xl + 8 * g : zero;
+    const int astep = rl <= 1 ? 32 : 0;
+
+    float acc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) acc[w] = 0.f;
+
     auto compute_stage = [&](int st, const RawTile (&r)[NW][kDepth]) {
 #pragma unroll
         for (int j = 0; j < kDepth; j++) {
@@ -210,10 +232,7 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
     };
 
     // Two register stages; whole pairs in the loop, the odd stage after it.
-    const int nst = (ntiles + kDepth - 1) / kDepth;
-    RawTile r0[NW][kDepth], r1[NW][kDepth];
     if (nst > 0) {
-        load_stage(0, r0);
         int st = 0;
         for (; st + 2 <= nst; st += 2) {
             load_stage(st + 1, r1);

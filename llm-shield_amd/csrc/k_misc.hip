@@ -58,12 +58,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
     float4 *h4 = (float4 *)(a.h + (size_t)row * a.D);
     const float4 *add4 = a.add ? (const float4 *)(a.add + (size_t)row * a.D) : nullptr;
     const size_t pstride = a.add_stride >> 2;
-    float4 x[kNormIters], p[kNormParts][kNormIters];
+    float4 x[kNormIters], p[kNormParts][kNormIters], wv[kNormIters];
+    const float4 *w4 = (const float4 *)a.w;
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
         if (256 * i >= ng) break;
         const int g = min(tid + 256 * i, ng - 1); // clamped: out-of-row lanes load and drop
         x[i] = h4[g];
+        wv[i] = w4[g];
     }
     if (add4) {
 #pragma unroll
@@ -113,13 +115,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
     __syncthreads();
     const float sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
     const float scale = 1.0f / sqrtf(sum / (float)a.D + a.eps);
-    const float4 *w4 = (const float4 *)a.w;
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
         if (256 * i >= ng) break;
         const int g = tid + 256 * i;
         const bool own = g < ng;
-        const float4 w = w4[min(g, ng - 1)];
+        const float4 w = wv[i];
         float y[4] = {(x[i].x * scale) * w.x, (x[i].y * scale) * w.y, (x[i].z * scale) * w.z, (x[i].w * scale) * w.w};
         if (a.out32 && own) *(float4 *)(a.out32 + (size_t)t * a.D + 4 * g) = make_float4(y[0], y[1], y[2], y[3]);
         if (a.ot) {
@@ -192,8 +193,9 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
 {
     __shared__ float cs[512], sn[512];
     const int t = blockIdx.x, tid = threadIdx.x;
-    const int pos = a.pos ? a.pos[t] : a.start + t;
-    const int slot = a.slot ? a.slot[t] : a.start + t;
+    const int start = a.start_dev ? *a.start_dev : a.start;
+    const int pos = a.pos ? a.pos[t] : start + t;
+    const int slot = a.slot ? a.slot[t] : start + t;
     const int qdim = a.n_heads * a.hd, kvdim = a.n_kv * a.hd;
     const int nq = qdim >> 1, nkv = kvdim >> 1, hpairs = a.hd >> 1;
     const float2 *qi = (const float2 *)(a.q_in + (size_t)t * a.ld_in);
@@ -373,6 +375,46 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *x, const int32
         ov[blockIdx.x] = sv[0];
         oi[blockIdx.x] = si[0];
     }
+}
+
+__global__ __launch_bounds__(256) void argmax_decode_kernel(const float *sv, const int32_t *si, int n, int32_t *state,
+                                                            int32_t *out)
+{
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int k = threadIdx.x; k < n; k += 256) better(v, idx, sv[k], si[k]);
+    bv[threadIdx.x] = v;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            float v1 = bv[threadIdx.x];
+            int i1 = bi[threadIdx.x];
+            better(v1, i1, bv[threadIdx.x + o], bi[threadIdx.x + o]);
+            bv[threadIdx.x] = v1;
+            bi[threadIdx.x] = i1;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int tok = bi[0];
+        out[state[1]] = tok;
+        state[2] = tok;
+        state[1] = state[1] + 1;
+        state[0] = state[0] + 1;
+    }
+}
+
+hipError_t launch_argmax_decode(const float *x, int n, float *sv, int32_t *si, int32_t *state, int32_t *out,
+                                hipStream_t s)
+{
+    const int blocks = 256;
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, x, (const int32_t *)nullptr, n, sv, si);
+    hipLaunchKernelGGL(argmax_decode_kernel, dim3(1), dim3(256), 0, s, (const float *)sv, (const int32_t *)si, blocks,
+                       state, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float *x, int n, int32_t *result, float *sv, int32_t *si, hipStream_t s)

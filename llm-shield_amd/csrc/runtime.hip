@@ -115,6 +115,7 @@ struct jev_ctx {
     DevBuf<float> h, y, yo, ydown, q, x32, ctx32, f32, xn, logits, part, xsum;
     DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
     DevBuf<int32_t> ints;
+    DevBuf<int32_t> att_ctr; // decode attention chunk counters (self-resetting, zeroed once)
     DevBuf<AttnTile> tiles;
     DevBuf<float> amax_v;
     DevBuf<int32_t> amax_i;
@@ -135,6 +136,7 @@ struct jev_ctx {
         double flops, bytes;
     };
     bool profiling = false;
+    bool capturing = false; // a graph capture is open on the stream (no event records)
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
     std::vector<ProfRec> prof;
@@ -208,7 +210,7 @@ struct ProfScope {
     hipEvent_t a = nullptr;
     ProfScope(jev_ctx *ctx, int k, double f, double b) : c(ctx), cls(k), flops(f), bytes(b)
     {
-        if (!c->profiling) return;
+        if (!c->profiling || c->capturing) return;
         a = next_event();
         (void)hipEventRecord(a, c->stream);
     }
@@ -369,6 +371,10 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
         HIP_TRY(c->ctx32.ensure((size_t)c->qdim()));
         HIP_TRY(c->f32.ensure((size_t)f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
+        if (c->att_ctr.n < (size_t)f.n_kv_heads) {
+            HIP_TRY(c->att_ctr.ensure((size_t)f.n_kv_heads));
+            HIP_TRY(hipMemset(c->att_ctr.p, 0, c->att_ctr.n * sizeof(int32_t)));
+        }
     } else {
         size_t T16 = ((size_t)T + 15) & ~(size_t)15;
         HIP_TRY(c->xt.ensure(T16 * std::max(f.hidden, c->qdim()) * 2));
@@ -531,7 +537,7 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
 
 // Enqueues the whole forward pass; the head output lands in `dout`
 // (device) or in ctx->logits / ctx->xn scratch.
-int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout)
+int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout, const int32_t *dpos = nullptr)
 {
     const jev_config &f = c->cfg;
     const int T = p.T, D = f.hidden, qdim = c->qdim(), kvdim = c->kvdim();
@@ -608,6 +614,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.pos = p.d_pos;
         ra.slot = p.d_slot;
         ra.start = p.start;
+        ra.start_dev = dpos;
         ra.freqs = c->freqs;
         ra.mscale = c->mscale;
         ra.orig_ctx = f.rope_original_context;
@@ -630,8 +637,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.shared_hi = p.d_shi;
             da.segment = p.d_seg;
             da.start = p.start;
+            da.start_dev = dpos;
             da.scale = scale;
             da.part = c->part.p;
+            da.counters = c->att_ctr.p;
             da.ctx = c->ctx32.p;
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                          8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
@@ -892,7 +901,7 @@ void jev_destroy(jev_ctx *c)
     if (c->vc) (void)hipFree(c->vc);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
-    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->att_ctr.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
     if (c->copied) (void)hipEventDestroy(c->copied);
@@ -1145,32 +1154,68 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     if (rc) return rc;
     if (n_steps <= 0 || !tokens_out) return fail(JEV_EINVAL, "bad arguments");
     if (first < 0 || first >= c->embd.rows) return fail(JEV_EINVAL, "Token id %d is outside the embedding table.", first);
-    DevBuf<int32_t> ids;
-    HIP_TRY(ids.ensure((size_t)n_steps + 1));
-    HIP_TRY(hipMemcpyAsync(ids.p, &first, sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
-    for (int i = 0; i < n_steps; i++) {
-        Plan p;
-        rc = prepare(c, ids.p + i, true, 1, nullptr, JEV_OUT_LAST_FULL, nullptr, 0, p);
-        if (!rc) rc = c->logits.ensure(std::max(c->logits.n, (size_t)c->cfg.vocab)) == hipSuccess ? JEV_OK
-                                                                                               : fail(JEV_ENOMEM, "logits");
-        if (!rc) rc = enqueue_forward(c, p, JEV_OUT_LAST_FULL, 0, c->logits.p);
-        if (rc) {
-            (void)hipStreamSynchronize(c->stream);
-            ids.release();
-            return rc;
+    // Every step is the same launch sequence: the token, the cache length and
+    // the output index live in device memory (state = {length, step, token})
+    // and the argmax kernel advances them.  The step is captured once as a
+    // HIP graph and replayed; with the per-kernel profiler on it is launched
+    // directly instead so every kernel is timed.
+    const int start = c->len, end = start + n_steps;
+    rc = kv_ensure(c, end);
+    if (rc) return rc;
+    DevBuf<int32_t> st;
+    HIP_TRY(st.ensure((size_t)n_steps + 3));
+    int32_t *state = st.p, *out = st.p + 3;
+    const int32_t init[3] = {start, 0, first};
+    HIP_TRY(hipMemcpy(state, init, sizeof(init), hipMemcpyHostToDevice));
+    Plan p;
+    rc = prepare(c, state + 2, true, 1, nullptr, JEV_OUT_LAST_FULL, nullptr, 0, p);
+    if (rc) return rc;
+    p.max_chunks = (end + 63) / 64; // grid for the longest step; shorter ones exit early
+    rc = ensure_workspace(c, 1, p.n_out, JEV_OUT_LAST_FULL, p.max_chunks);
+    if (!rc && c->logits.ensure(std::max(c->logits.n, (size_t)c->cfg.vocab)) != hipSuccess) rc = fail(JEV_ENOMEM, "logits");
+    if (rc) return rc;
+    auto step = [&]() -> int {
+        int r = enqueue_forward(c, p, JEV_OUT_LAST_FULL, 0, c->logits.p, state);
+        if (r) return r;
+        hipError_t e = launch_argmax_decode(c->logits.p, c->cfg.vocab, c->amax_v.p, c->amax_i.p, state, out, c->stream);
+        return e == hipSuccess ? JEV_OK : fail(JEV_EDEVICE, "argmax: %s", hipGetErrorString(e));
+    };
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (!c->profiling) {
+        HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        c->capturing = true;
+        rc = step();
+        c->capturing = false;
+        hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "graph capture: %s", hipGetErrorString(e));
+        if (!rc && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+            rc = fail(JEV_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    }
+    int done = 0;
+    for (; !rc && done < n_steps; done++) {
+        if (c->cancel.exchange(0)) {
+            rc = fail(JEV_ECANCELED, "greedy decoding was cancelled after %d steps", done);
+            break;
         }
-        c->len = std::max(c->len, p.end);
-        hipError_t e = launch_argmax(c->logits.p, c->cfg.vocab, ids.p + i + 1, c->amax_v.p, c->amax_i.p, c->stream);
-        if (e != hipSuccess) {
-            ids.release();
-            return fail(JEV_EDEVICE, "argmax: %s", hipGetErrorString(e));
+        if (exec) {
+            hipError_t e = hipGraphLaunch(exec, c->stream);
+            if (e != hipSuccess) rc = fail(JEV_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+        } else {
+            rc = step();
         }
     }
-    hipError_t e = hipMemcpyAsync(tokens_out, ids.p + 1, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, c->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    ids.release();
-    if (e != hipSuccess) return fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
-    return JEV_OK;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+    c->len = std::max(c->len, start + done - (rc && rc != JEV_ECANCELED ? 1 : 0));
+    if (!rc) {
+        e = hipMemcpy(tokens_out, out, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+    }
+    st.release();
+    return rc;
 }
 
 int jev_margins(const float *v, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature, float *margins,
