@@ -81,6 +81,32 @@ __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, i
 // loop free of divergent loads lets the compiler count outstanding loads
 // exactly instead of draining the queue every stage.
 
+// B fragment of block bb of a loaded chunk: 8 fp16 integers for the lane's
+// row at k = 8g .. 8g + 7.
+template <int TYPE>
+__device__ __forceinline__ half8_t decode_b_frag(const BChunk &c, int bb)
+{
+    uint32_t o0, o1, o2, o3;
+    if (TYPE == kQ8_0) {
+        const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
+        bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
+        bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
+    } else {
+        const uint32_t w = bb ? c.q.y : c.q.x;
+        uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
+        _Float16 bias = (_Float16)1032.0f;
+        if (TYPE == kQ5_1) {
+            const uint32_t hb = (c.qh >> (8 * bb)) & 0xffu;
+            n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
+            n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
+            bias = (_Float16)1024.0f;
+        }
+        bytes_to_f16(n0, bias, o0, o1);
+        bytes_to_f16(n1, bias, o2, o3);
+    }
+    return __builtin_bit_cast(half8_t, make_uint4(o0, o1, o2, o3));
+}
+
 // Decoded quants of one chunk as fp16 integers: block 0 to dst[0..8),
 // block 1 to dst[32..40) (the LDS row of the chunk's weight row).
 template <int TYPE>
@@ -434,6 +460,279 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     }
 }
 
+// ---------------------------------------------------------------------------
+// B-direct variant: the four waves sit side by side along N, each owning TN
+// weight tiles (16 rows each) that it streams from HBM straight into
+// registers and decodes there -- a tile slot is exactly the lane's B fragment
+// -- while the BM x 64 activation tile of a stage is loaded once per
+// workgroup into LDS and read by all four waves.  Per MFMA this moves half
+// the bytes through the vector-memory path and the LDS of the variant above
+// (whose B tile goes through LDS and whose A fragments come per wave from
+// L2).  The arithmetic per output is the same sequence of MFMAs and FMAs, so
+// the two variants agree bit for bit and either may serve any M.
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, int nt, int gm)
+{
+    constexpr int BM = 16 * TM, BN = 64 * TN;
+    constexpr int U = PD + 1; // weight register ring
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * 4 * 512]; // [mi][block][part] operand tiles
+
+    // ---- tile of this workgroup (same order and K splits as gemm_q_kernel)
+    const int total = gridDim.x;
+    const int per_xcd = total >> 3;
+    const int L = blockIdx.x;
+    int Lp = (L & 7) * per_xcd + (L >> 3);
+    const int tiles8 = total / a.ksplit;
+    const int z = Lp / tiles8;
+    Lp -= z * tiles8;
+    const int group = gm * nt;
+    const int first_m = (Lp / group) * gm;
+    const int gsz = min(mt - first_m, gm);
+    if (gsz <= 0) return;
+    const int tile_m = first_m + (Lp % group) % gsz;
+    const int tile_n = (Lp % group) / gsz;
+    if (tile_m >= mt || tile_n >= nt) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = a.M, K = a.K, nblk = K >> 5;
+    const int nb_per = gemm_split_blocks(nblk, a.ksplit);
+    const int kb_begin = z * nb_per;
+    const int nb = min(nblk - kb_begin, nb_per);
+    const int nstage = (nb + 1) >> 1;
+    const int m0 = tile_m * BM;
+
+    // ---- activation loader: thread -> fragment f = tid / 64 (block f >> 1,
+    // part f & 1) of every row group mi, lane slot tid % 64: 16 bytes each.
+    const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
+    const rsrc_t ra = make_rsrc(a.xt, (uint32_t)(rg_last + 1) * nblk * 2048);
+    const int af = tid >> 6, abb = af >> 1, apart = af & 1;
+    uint32_t va[TM];
+#pragma unroll
+    for (int mi = 0; mi < TM; mi++)
+        va[mi] = (((uint32_t)min((m0 >> 4) + mi, rg_last) * nblk * 2 + apart) * 512 + lane * 8) * 2;
+    auto load_a = [&](int st, uint4 (&r)[TM]) __attribute__((always_inline)) {
+        st = min(st, nstage - 1);
+        const int kblk = kb_begin + min(2 * st + abb, nb - 1);
+#pragma unroll
+        for (int mi = 0; mi < TM; mi++)
+            r[mi] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi], kblk * 2048, 0));
+    };
+    auto store_a = [&](int buf, const uint4 (&r)[TM]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mi = 0; mi < TM; mi++) *(uint4 *)&As[buf][(mi * 4 + af) * 512 + lane * 8] = r[mi];
+    };
+
+    // ---- weight loader: tile n of this wave is tile row wave * TN + n of the workgroup
+    rsrc_t rq[TN], rd[TN], rm[TN], rh[TN];
+    int btile0[TN];
+    const uint32_t vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
+#pragma unroll
+    for (int n = 0; n < TN; n++) {
+        const int t = wave * TN + n;
+        int seg, rgw;
+        if (MODE == kGemmSwiGlu) {
+            seg = t & 1; // 16-row groups alternate gate and up
+            rgw = tile_n * (BN / 32) + (t >> 1);
+        } else {
+            int s0 = 0, start = 0, n0 = tile_n * BN;
+            while (s0 + 1 < a.nseg && n0 >= start + a.seg[s0].rows) {
+                start += a.seg[s0].rows;
+                s0++;
+            }
+            seg = s0;
+            rgw = (n0 - start) / 16 + t;
+        }
+        seg = __builtin_amdgcn_readfirstlane(seg);
+        const QWeight &w = a.seg[seg];
+        const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
+        const uint32_t tiles = (uint32_t)RG * KP;
+        rq[n] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
+        rd[n] = make_rsrc(w.d, tiles * 64);
+        if (TYPE == kQ5_1) {
+            rm[n] = make_rsrc(w.m, tiles * 64);
+            rh[n] = make_rsrc(w.qh, tiles * 128);
+        }
+        btile0[n] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + (kb_begin >> 1));
+    }
+    auto load_b = [&](int st, BChunk (&br)[TN]) __attribute__((always_inline)) {
+        st = min(st, nstage - 1);
+#pragma unroll
+        for (int n = 0; n < TN; n++) {
+            const int tile = btile0[n] + st;
+            if (TYPE == kQ8_0) {
+                br[n].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[n], vq, tile * 1024, 0));
+            } else {
+                uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[n], vq, tile * 512, 0));
+                br[n].q = make_uint4(v.x, v.y, 0u, 0u);
+            }
+            br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
+            if (TYPE == kQ5_1) {
+                br[n].m = __builtin_amdgcn_raw_buffer_load_b32(rm[n], vd, tile * 64, 0);
+                br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
+            }
+        }
+    };
+    // Q5_1 block sums of the lane's four C rows
+    rsrc_t rs;
+    uint32_t vs[TM];
+    if (TYPE == kQ5_1) {
+        rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
+#pragma unroll
+        for (int mi = 0; mi < TM; mi++) vs[mi] = (uint32_t)(m0 + mi * 16 + 4 * (lane >> 4)) * nblk * 4;
+    }
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int st, int buf, const BChunk (&br)[TN]) __attribute__((always_inline)) {
+        const bool second = 2 * st + 1 < nb;
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            if (bb == 1 && !second) break; // odd block count: no second block
+            half8_t bf[TN];
+            float dv[TN], mv[TN];
+#pragma unroll
+            for (int n = 0; n < TN; n++) {
+                bf[n] = decode_b_frag<TYPE>(br[n], bb);
+                dv[n] = h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d));
+                if (TYPE == kQ5_1) mv[n] = h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m));
+            }
+#pragma unroll
+            for (int mi = 0; mi < TM; mi++) {
+                const half8_t ah = *(const half8_t *)&As[buf][(mi * 4 + bb * 2 + 0) * 512 + lane * 8];
+                const half8_t al = *(const half8_t *)&As[buf][(mi * 4 + bb * 2 + 1) * 512 + lane * 8];
+                floatx4 xs4;
+                if (TYPE == kQ5_1) {
+                    const int kblk = kb_begin + 2 * st + bb;
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        xs4[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs[mi] + r * nblk * 4, kblk * 4, 0));
+                }
+#pragma unroll
+                for (int n = 0; n < TN; n++) {
+                    floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[n], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[n], p, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        float v = fmaf(dv[n], p[r], acc[mi][n][r]);
+                        if (TYPE == kQ5_1) v = fmaf(mv[n], xs4[r], v);
+                        acc[mi][n][r] = v;
+                    }
+                }
+            }
+        }
+    };
+
+    // ---- pipeline: activations one stage ahead through LDS (double
+    // buffered), weights U stages ahead in a register ring.  Whole groups of
+    // U stages in the loop, the remainder after it (see gemm_q_kernel).
+    BChunk br[U][TN];
+    uint4 araw[TM];
+    load_a(0, araw);
+#pragma unroll
+    for (int j = 0; j < U; j++) load_b(j, br[j]);
+    store_a(0, araw);
+    load_a(1, araw);
+    __syncthreads();
+    auto stage = [&](auto jc, int s) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        compute(s, s & 1, br[j]);
+        store_a((s + 1) & 1, araw);
+        load_a(s + 2, araw);
+        load_b(s + U, br[j]);
+        __syncthreads();
+    };
+    const int ngroups = nstage / U;
+    int s0 = 0;
+    for (int g = 0; g < ngroups; g++, s0 += U) {
+        stage(std::integral_constant<int, 0>{}, s0);
+        if constexpr (U > 1) stage(std::integral_constant<int, 1 % U>{}, s0 + 1);
+        if constexpr (U > 2) stage(std::integral_constant<int, 2 % U>{}, s0 + 2);
+        if constexpr (U > 3) stage(std::integral_constant<int, 3 % U>{}, s0 + 3);
+        static_assert(U <= 4, "ring deeper than the unrolled group");
+    }
+    {
+        const int rem = nstage - s0;
+        if constexpr (U > 1) if (rem > 0) stage(std::integral_constant<int, 0>{}, s0);
+        if constexpr (U > 2) if (rem > 1) stage(std::integral_constant<int, 1 % U>{}, s0 + 1);
+        if constexpr (U > 3) if (rem > 2) stage(std::integral_constant<int, 2 % U>{}, s0 + 2);
+    }
+
+    // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
+    const int row_base = m0 + 4 * (lane >> 4);
+    if (MODE == kGemmStore) {
+        float *y = a.y + (size_t)z * M * a.ldy;
+        int seg = 0, start = 0;
+        const int n0 = tile_n * BN;
+        while (seg + 1 < a.nseg && n0 >= start + a.seg[seg].rows) {
+            start += a.seg[seg].rows;
+            seg++;
+        }
+        const QWeight &ws = a.seg[seg];
+#pragma unroll
+        for (int n = 0; n < TN; n++) {
+            const int off = (wave * TN + n) * 16 + (lane & 15);
+            if (n0 - start + off >= ws.rows) continue;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = row_base + 16 * i + r;
+                    if (row < M) y[(size_t)row * a.ldy + n0 + off] = acc[i][n][r];
+                }
+        }
+    } else {
+        const int ld = a.seg[0].rows;
+#pragma unroll
+        for (int pp = 0; pp < TN / 2; pp++) {
+            // tiles 2pp (gate) and 2pp+1 (up) of this wave cover the same outputs
+            const int col = tile_n * (BN / 2) + ((wave * TN + 2 * pp) >> 1) * 16 + (lane & 15);
+            if (col >= ld) continue;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = row_base + 16 * i + r;
+                    if (row >= M) continue;
+                    // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g).
+                    const float g = acc[i][2 * pp][r], u = acc[i][2 * pp + 1][r];
+                    const float gu = g * u;
+                    const float e = expf(-g);
+                    const float sg = 1.0f / (1.0f + e);
+                    const float v = sg * gu;
+                    uint16_t hi, lo;
+                    split_f16(v, hi, lo);
+                    a.ot[xt_index(row, col, ld >> 5, 0)] = hi;
+                    a.ot[xt_index(row, col, ld >> 5, 1)] = lo;
+                }
+        }
+    }
+}
+
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC>
+static hipError_t launch_bd(const GemmArgs &a, hipStream_t s)
+{
+    constexpr int BM = 16 * TM, BN = 64 * TN;
+    static_assert(MODE != kGemmSwiGlu || TN % 2 == 0, "SwiGLU pairs tiles within a wave");
+    int mt = (a.M + BM - 1) / BM;
+    int ncols;
+    if (MODE == kGemmSwiGlu) {
+        ncols = (a.seg[0].rows + BN / 2 - 1) / (BN / 2);
+    } else {
+        int ntot = 0;
+        for (int i = 0; i < a.nseg; i++) ntot += a.seg[i].rows;
+        ncols = (ntot + BN - 1) / BN;
+    }
+    int gm = mt <= 8 ? mt : 8;
+    int tiles = mt * ncols;
+    int grid = ((tiles + 7) & ~7) * a.ksplit;
+    hipLaunchKernelGGL((gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC>), dim3(grid), dim3(256), 0, s, a, mt, ncols, gm);
+    return hipGetLastError();
+}
+
 template <int TYPE, int MODE, int WM, int WN, int TM, int TN, int PD, int KS, int OCC>
 static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
 {
@@ -461,7 +760,20 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
 #ifdef JEV_GEMM_CFG
     return JEV_GEMM_CFG(a, s);
 #endif
-    if (a.M <= 512) return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
+#ifdef JEV_GEMM_BD
+    return JEV_GEMM_BD(a, s);
+#endif
+    // Measured on MI355X (3B shapes, Q8_0): small batches fill the chip with
+    // 64 x 64 tiles, except the SwiGLU pair, where B-direct 32 x 128 tiles are
+    // faster; large batches take B-direct 64 x 256 tiles.  B-direct needs the
+    // store-mode segments to split on 256-row boundaries.
+    bool bd_ok = true;
+    for (int i = 0; i + 1 < a.nseg; i++) bd_ok = bd_ok && a.seg[i].rows % 256 == 0;
+    if (a.M <= 512) {
+        if (MODE == kGemmSwiGlu) return launch_bd<TYPE, MODE, 2, 2, 1, 4>(a, s);
+        return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
+    }
+    if (bd_ok) return launch_bd<TYPE, MODE, 4, 4, 1, 2>(a, s);
     return launch_cfg<TYPE, MODE, 4, 1, 2, 8, 1, 1, 2>(a, s);
 }
 
