@@ -103,64 +103,69 @@ __global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
     for (int j = 0; j < 8; j++) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
 
-    for (int b = 0; b < nblocks; b++) {
-        __syncthreads();
-        // Stage K: thread -> (key, quarter row) as pairs in [key][dim].
+    // Staging.  K: thread -> (key tid / 4, quarter row) as pairs in
+    // [key][dim].  V transposed to [dim][key]: thread -> 4 keys (4 (tid % 16)
+    // ..) x 8 dims (8 (tid / 16) ..), so a wave's stores spread over the
+    // banks.  The next block's rows are loaded into registers while the
+    // current block is on the matrix cores; loads are unconditional (the key
+    // clamped, the value zeroed past the end when stored).
+    const int kkey = tid >> 2, kpart = tid & 3;
+    const int vkq = tid & 15, vdq = tid >> 4;
+    float4 kr[8], vr[4][2];
+    auto slot_of = [&](int kl) { return kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh); };
+    auto load_kv = [&](int b) __attribute__((always_inline)) {
+        const int kl = min(b * KB + kkey, max_limit - 1);
+        const float4 *ks = (const float4 *)(kbase + (size_t)slot_of(kl) * 128 + kpart * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = ks[i];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int vl = min(b * KB + 4 * vkq + kk, max_limit - 1);
+            const float4 *vs = (const float4 *)(vbase + (size_t)slot_of(vl) * 128 + 8 * vdq);
+            vr[kk][0] = vs[0];
+            vr[kk][1] = vs[1];
+        }
+    };
+    auto store_kv = [&](int b) __attribute__((always_inline)) {
         {
-            int key = tid >> 2, part = tid & 3;
-            const bool ok = b * KB + key < max_limit;
-            const int kl = min(b * KB + key, max_limit - 1);
-            uint2 hv[8], lv[8];
-            {
-                const int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
-                const float4 *ks = (const float4 *)(kbase + (size_t)p * 128 + part * 32);
-                float4 kr[8];
+            const bool ok = b * KB + kkey < max_limit;
+            uint2 *kh2 = (uint2 *)(Kh + kkey * KROW + kpart * 32);
+            uint2 *kl2 = (uint2 *)(Kl + kkey * KROW + kpart * 32);
 #pragma unroll
-                for (int i = 0; i < 8; i++) kr[i] = ks[i];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    split4(kr[i], hv[i], lv[i]);
-                    if (!ok) hv[i] = lv[i] = make_uint2(0u, 0u);
-                }
-            }
-            uint4 *kh4 = (uint4 *)(Kh + key * KROW + part * 32);
-            uint4 *kl4 = (uint4 *)(Kl + key * KROW + part * 32);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                kh4[i] = make_uint4(hv[2 * i].x, hv[2 * i].y, hv[2 * i + 1].x, hv[2 * i + 1].y);
-                kl4[i] = make_uint4(lv[2 * i].x, lv[2 * i].y, lv[2 * i + 1].x, lv[2 * i + 1].y);
+            for (int i = 0; i < 8; i++) {
+                uint2 hv, lv;
+                split4(kr[i], hv, lv);
+                kh2[i] = make_uint2(ok ? hv.x : 0u, ok ? hv.y : 0u);
+                kl2[i] = make_uint2(ok ? lv.x : 0u, ok ? lv.y : 0u);
             }
         }
-        // Stage V transposed: thread -> 4 keys x 8 dims, written as [dim][key].
-        // Loads are unconditional (clamped key, value zeroed past the end) so
-        // all four keys' rows are in flight together.
         {
-            int kg = tid >> 4, dg = tid & 15;
             float vv[4][8];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const int kl = min(b * KB + 4 * kg + kk, max_limit - 1);
-                const int p = kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh);
-                const float4 *vs = (const float4 *)(vbase + (size_t)p * 128 + 8 * dg);
-                const float4 v0 = vs[0], v1 = vs[1];
-                vv[kk][0] = v0.x; vv[kk][1] = v0.y; vv[kk][2] = v0.z; vv[kk][3] = v0.w;
-                vv[kk][4] = v1.x; vv[kk][5] = v1.y; vv[kk][6] = v1.z; vv[kk][7] = v1.w;
-            }
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const bool ok = b * KB + 4 * kg + kk < max_limit;
-#pragma unroll
-                for (int i = 0; i < 8; i++) vv[kk][i] = ok ? vv[kk][i] : 0.f;
+                const bool ok = b * KB + 4 * vkq + kk < max_limit;
+                const float4 v0 = vr[kk][0], v1 = vr[kk][1];
+                vv[kk][0] = ok ? v0.x : 0.f; vv[kk][1] = ok ? v0.y : 0.f;
+                vv[kk][2] = ok ? v0.z : 0.f; vv[kk][3] = ok ? v0.w : 0.f;
+                vv[kk][4] = ok ? v1.x : 0.f; vv[kk][5] = ok ? v1.y : 0.f;
+                vv[kk][6] = ok ? v1.z : 0.f; vv[kk][7] = ok ? v1.w : 0.f;
             }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 uint2 hv, lv;
                 split4(make_float4(vv[0][i], vv[1][i], vv[2][i], vv[3][i]), hv, lv);
-                *(uint2 *)(Vh + (8 * dg + i) * VROW + 4 * kg) = hv;
-                *(uint2 *)(Vl + (8 * dg + i) * VROW + 4 * kg) = lv;
+                *(uint2 *)(Vh + (8 * vdq + i) * VROW + 4 * vkq) = hv;
+                *(uint2 *)(Vl + (8 * vdq + i) * VROW + 4 * vkq) = lv;
             }
         }
+    };
+
+    load_kv(0);
+    for (int b = 0; b < nblocks; b++) {
+        __syncthreads(); // the previous block's fragments have been read
+        store_kv(b);
         __syncthreads();
+        load_kv(min(b + 1, nblocks - 1)); // in flight during this block's math
 
         // S^T for 4 sub-blocks of 16 keys.
         floatx4 sc[4];
