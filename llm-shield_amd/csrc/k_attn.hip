@@ -42,15 +42,17 @@ constexpr int VROW = KB + 8;    // transposed V pair LDS row, halves
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
+// x = hi + lo as fp16 pairs: hi rounded toward zero (two per v_cvt_pkrtz),
+// lo the remainder rounded the same way; |x - hi - lo| < 2^-20 |x| for normal fp16 hi.
 __device__ __forceinline__ void split4(float4 v, uint2 &hi, uint2 &lo)
 {
-    uint16_t h0, l0, h1, l1, h2, l2, h3, l3;
-    split_f16(v.x, h0, l0);
-    split_f16(v.y, h1, l1);
-    split_f16(v.z, h2, l2);
-    split_f16(v.w, h3, l3);
-    hi = make_uint2((uint32_t)h0 | ((uint32_t)h1 << 16), (uint32_t)h2 | ((uint32_t)h3 << 16));
-    lo = make_uint2((uint32_t)l0 | ((uint32_t)l1 << 16), (uint32_t)l2 | ((uint32_t)l3 << 16));
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    const fp16x2 h01 = __builtin_amdgcn_cvt_pkrtz(v.x, v.y), h23 = __builtin_amdgcn_cvt_pkrtz(v.z, v.w);
+    const float r0 = v.x - (float)h01[0], r1 = v.y - (float)h01[1];
+    const float r2 = v.z - (float)h23[0], r3 = v.w - (float)h23[1];
+    const fp16x2 l01 = __builtin_amdgcn_cvt_pkrtz(r0, r1), l23 = __builtin_amdgcn_cvt_pkrtz(r2, r3);
+    hi = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+    lo = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
 }
 
 __device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
@@ -198,13 +200,13 @@ __global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
         float m_new = fmaxf(m_run, bmax);
-        float alpha = expf(m_run - m_new);
+        float alpha = __expf(m_run - m_new);
         float psum = 0.f;
 #pragma unroll
         for (int s = 0; s < 4; s++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                float p = expf(sc[s][r] - m_new);
+                float p = __expf(sc[s][r] - m_new);
                 sc[s][r] = p;
                 psum += p;
             }
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
             sc = acc * a.scale;
         }
         const float mx = warp_max(sc);
-        const float p = lane < nk ? expf(sc - mx) : 0.f;
+        const float p = lane < nk ? __expf(sc - mx) : 0.f;
         const float sum = warp_sum(p);
         ps[wave][lane] = p;
         __syncthreads();
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 if (c0 + j < nchunks) {
-                    const float f = expf(mv[j] - M);
+                    const float f = __expf(mv[j] - M);
                     L = fmaf(lv[j], f, L);
                     O0 = fmaf(ov[j].x, f, O0);
                     O1 = fmaf(ov[j].y, f, O1);
