@@ -4,13 +4,20 @@
 Headline (the reference's own benchmark, `jev bench` prefill): a 256-token
 causal prefill of the 26-layer Ministral-3 3B shape with Q8_0 weights, ending
 in the final position's full-vocabulary logits.  value = prompt tokens per
-second with the token ids and the model already resident in HBM.  Beside it,
-the 4096-token-trunk, 9 x 48-token-branch tree decision (verdict rows only) in
-ms per decision.
+second with the token ids and the model already resident in HBM.  Beside it:
+  * the 4096-token-trunk, 9 x 48-token-branch tree decision (Q8_0, verdict
+    rows only) in ms per decision;
+  * the Q5_1 decode loop: 512-token prefill, then 128 greedy steps, ms per
+    token and the decode GEMVs' achieved HBM bandwidth;
+  * 64 independent Q4_0 decisions (512-token trunk + 5 x 32-token branches
+    each) evaluated in one tree-masked pass, decisions per second;
+  * the repo's single Q8_0 matmul (3072 x 3072 weight, 256 tokens), TFLOP/s,
+    beside the oracle's GFLOP/s on 1 and on all host threads.
 
-Weights are synthetic (N(0, 0.02) quantized to Q8_0 with the ggml reference
-quantizer, norms 1.0) because no checkpoint is available offline; token ids are
-uniform on the vocabulary.
+Weights are synthetic (N(0, 0.02) quantized with the ggml reference quantizer,
+norms 1.0) because no checkpoint is available offline; token ids are uniform on
+the vocabulary.  Timed loops run without the per-kernel profiler; the kernel
+breakdowns come from a separate profiled pass over the same work.
 
 One JSON line goes to stdout; progress goes to stderr.
 """
@@ -40,6 +47,39 @@ def prof_read(lib, h, cls):
     return n.value, ms.value, fl.value, by.value
 
 
+def batched_decisions_layout(nd, trunk_n, nb, bl):
+    """Token layout of nd independent trees laid end to end in one KV arena:
+    decision d owns slots [d * per, (d + 1) * per); its trunk is causal from
+    position 0, each branch sees the trunk and itself (positions continue from
+    the trunk), outputs are the branches' last tokens."""
+    import numpy as np
+    import jev
+
+    per = trunk_n + nb * bl
+    total = nd * per
+    slot = np.arange(total, dtype=np.int32)
+    pos = np.empty(total, np.int32)
+    lo = np.empty(total, np.int32)
+    hi = np.empty(total, np.int32)
+    seg = np.empty(total, np.int32)
+    outs = []
+    for d in range(nd):
+        b0 = d * per
+        t = np.arange(trunk_n)
+        pos[b0:b0 + trunk_n] = t
+        lo[b0:b0 + trunk_n] = b0
+        hi[b0:b0 + trunk_n] = b0
+        seg[b0:b0 + trunk_n] = b0
+        for b in range(nb):
+            s0 = b0 + trunk_n + b * bl
+            pos[s0:s0 + bl] = trunk_n + np.arange(bl)
+            lo[s0:s0 + bl] = b0
+            hi[s0:s0 + bl] = b0 + trunk_n
+            seg[s0:s0 + bl] = s0
+            outs.append(s0 + bl - 1)
+    return jev.TokenLayout(slot, pos, hi, seg, np.array(outs, np.int32), total, shared_lo=lo)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -48,6 +88,9 @@ def main():
     ap.add_argument("--tree-steps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
     ap.add_argument("--no-tree", action="store_true", help="skip the tree-decision leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the Q5_1 decode leg")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched Q4_0 decisions leg")
+    ap.add_argument("--no-matmul", action="store_true", help="skip the single-matmul leg")
     ap.add_argument("--layers", type=int, default=26, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -84,8 +127,7 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    L.check(lib.jev_profile_enable(h, 1))
+    L.check(lib.jev_sync(h))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -93,14 +135,20 @@ def main():
     L.check(lib.jev_sync(h))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    gemm = prof_read(lib, h, L.PROF_GEMM)
-    attn = prof_read(lib, h, L.PROF_ATTN)
-    gemv = prof_read(lib, h, L.PROF_GEMV)
-    L.check(lib.jev_profile_enable(h, 0))
     ms_step = elapsed / args.steps * 1e3
     tok_s = T * args.steps / elapsed
     log(f"prefill {T} tokens: {ms_step:.3f} ms/step, {tok_s:,.0f} tok/s")
     gpu_logits = d_out.cpu().numpy()
+    # profiled pass (HIP events around every kernel class) for the breakdown
+    prof_steps = min(args.steps, 5)
+    L.check(lib.jev_profile_enable(h, 1))
+    for _ in range(prof_steps):
+        step()
+    L.check(lib.jev_sync(h))
+    gemm = prof_read(lib, h, L.PROF_GEMM)
+    attn = prof_read(lib, h, L.PROF_ATTN)
+    gemv = prof_read(lib, h, L.PROF_GEMV)
+    L.check(lib.jev_profile_enable(h, 0))
 
     gemm_avg_ms = gemm[1] / max(gemm[0], 1)
     gemm_tflops = gemm[2] / (gemm[1] * 1e-3) / 1e12 if gemm[1] > 0 else 0.0
@@ -135,15 +183,15 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops * 1e12 / PEAK_FP16_MFMA, 4),
             "traffic": traffic,
-            "launches": gemm[0] // args.steps,
+            "launches": gemm[0] // prof_steps,
             "avg_launch_us": round(gemm_avg_ms * 1e3, 2),
             "flops_per_launch": gemm[2] / max(gemm[0], 1),
             "alg_bytes_per_launch": round(gemm[3] / max(gemm[0], 1)),
         },
         "breakdown_ms_per_step": {
-            "gemm": round(gemm[1] / args.steps, 4),
-            "attention": round(attn[1] / args.steps, 4),
-            "gemv_head": round(gemv[1] / args.steps, 4),
+            "gemm": round(gemm[1] / prof_steps, 4),
+            "attention": round(attn[1] / prof_steps, 4),
+            "gemv_head": round(gemv[1] / prof_steps, 4),
         },
     }
 
@@ -165,14 +213,18 @@ def main():
                                            ctypes.c_void_p(d_v.data_ptr())))
 
         decide()
+        L.check(lib.jev_sync(h))
         torch.cuda.synchronize()
-        L.check(lib.jev_profile_enable(h, 1))
         t0 = time.perf_counter()
         for _ in range(args.tree_steps):
             decide()
         L.check(lib.jev_sync(h))
         torch.cuda.synchronize()
         tree_ms = (time.perf_counter() - t0) / args.tree_steps * 1e3
+        L.check(lib.jev_profile_enable(h, 1))
+        for _ in range(args.tree_steps):
+            decide()
+        L.check(lib.jev_sync(h))
         tg = prof_read(lib, h, L.PROF_GEMM)
         ta = prof_read(lib, h, L.PROF_ATTN)
         L.check(lib.jev_profile_enable(h, 0))
@@ -187,6 +239,156 @@ def main():
             "attention_tflops": round(ta[2] / (ta[1] * 1e-3) / 1e12, 2) if ta[1] else None,
         }
         result["tree_z"] = [round(float(x), 5) for x in z]
+
+    model.close()
+
+    # ---- Q5_1 decode loop: 512-token prefill, 128 greedy steps
+    if not args.no_decode:
+        dcfg = jev.ModelConfig(n_layers=args.layers, initial_kv_capacity=1024)
+        t0 = time.time()
+        dsynth = jev.SynthModel(dcfg, jev.TYPE_Q5_1)
+        dmodel = dsynth.open(0)
+        log(f"synthetic Q5_1 model ready in {time.time() - t0:.1f}s")
+        dh = dmodel.handle
+        prompt = jev.random_tokens(512, dcfg.vocab, 31)
+        n_dec = 128
+
+        def decode_run():
+            L.check(lib.jev_kv_reset(dh))
+            dmodel.prefill(prompt)
+            L.check(lib.jev_sync(dh))
+            t = time.perf_counter()
+            out = dmodel.decode_greedy(int(prompt[-1]), n_dec)
+            return time.perf_counter() - t, out
+
+        decode_run()
+        dt, toks = decode_run()
+        ms_tok = dt / n_dec * 1e3
+        L.check(lib.jev_kv_reset(dh))
+        dmodel.prefill(prompt)
+        L.check(lib.jev_sync(dh))
+        L.check(lib.jev_profile_enable(dh, 1))
+        dmodel.decode_greedy(int(prompt[-1]), n_dec)
+        gv = prof_read(lib, dh, L.PROF_GEMV)
+        da = prof_read(lib, dh, L.PROF_DECODE_ATTN)
+        L.check(lib.jev_profile_enable(dh, 0))
+        gemv_gbs = gv[3] / (gv[1] * 1e-3) / 1e9 if gv[1] else 0.0
+        log(f"Q5_1 decode: {ms_tok:.3f} ms/token ({1e3 / ms_tok:.1f} tok/s); GEMV {gemv_gbs:.0f} GB/s "
+            f"({gv[1] / n_dec:.3f} ms/token), attention {da[1] / n_dec:.3f} ms/token")
+        result["decode_q5_1"] = {
+            "workload": "Q5_1 3B shape, 512-token prefill then 128 greedy decode steps (fp32 KV cache)",
+            "ms_per_token": round(ms_tok, 4),
+            "tok_s": round(1e3 / ms_tok, 2),
+            "gemv_ms_per_token": round(gv[1] / n_dec, 4),
+            "gemv_gbs": round(gemv_gbs, 1),
+            "gemv_hbm_frac": round(gemv_gbs * 1e9 / PEAK_HBM, 4),
+            "decode_attention_ms_per_token": round(da[1] / n_dec, 4),
+            "first_tokens": [int(x) for x in toks[:8]],
+        }
+        dmodel.close()
+        del dsynth
+
+    # ---- 64 independent Q4_0 decisions in one tree-masked pass
+    if not args.no_batched:
+        nd, trunk_n, nb, bl = 64, 512, 5, 32
+        per = trunk_n + nb * bl
+        total = nd * per
+        bcfg = jev.ModelConfig(n_layers=args.layers, initial_kv_capacity=total)
+        t0 = time.time()
+        bsynth = jev.SynthModel(bcfg, jev.TYPE_Q4_0)
+        bmodel = bsynth.open(0)
+        log(f"synthetic Q4_0 model ready in {time.time() - t0:.1f}s")
+        bh = bmodel.handle
+        lay = batched_decisions_layout(nd, trunk_n, nb, bl)
+        lay_c = lay.to_c()
+        rows = np.array([jev.VERDICT_YES, jev.VERDICT_NO], np.int32)
+        btoks = jev.random_tokens(total, bcfg.vocab, 47)
+        d_bt = torch.from_numpy(btoks).to(dev)
+        d_bv = torch.empty(nd * nb * 2, dtype=torch.float32, device=dev)
+
+        def batch():
+            L.check(lib.jev_kv_reset(bh))
+            L.check(lib.jev_forward_device(bh, ctypes.c_void_p(d_bt.data_ptr()), total, ctypes.byref(lay_c),
+                                           L.OUT_SELECTED, rows.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), 2,
+                                           ctypes.c_void_p(d_bv.data_ptr())))
+
+        batch()
+        L.check(lib.jev_sync(bh))
+        reps = 2
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            batch()
+        L.check(lib.jev_sync(bh))
+        b_ms = (time.perf_counter() - t0) / reps * 1e3
+        L.check(lib.jev_profile_enable(bh, 1))
+        batch()
+        L.check(lib.jev_sync(bh))
+        bg = prof_read(lib, bh, L.PROF_GEMM)
+        ba = prof_read(lib, bh, L.PROF_ATTN)
+        L.check(lib.jev_profile_enable(bh, 0))
+        zb = d_bv.cpu().numpy().reshape(nd, nb, 2)
+        log(f"64 Q4_0 decisions: {b_ms:.1f} ms per batch, {nd / b_ms * 1e3:.1f} decisions/s; "
+            f"gemm {bg[1]:.1f} ms, attention {ba[1]:.1f} ms")
+        result["batched_q4_0"] = {
+            "workload": "64 independent decisions, each a 512-token trunk + 5 x 32-token branches, Q4_0 3B shape, "
+                        "verdict rows only, one tree-masked pass of 43008 tokens",
+            "ms_per_batch": round(b_ms, 2),
+            "decisions_per_s": round(nd / b_ms * 1e3, 2),
+            "gemm_ms": round(bg[1], 2),
+            "gemm_tflops": round(bg[2] / (bg[1] * 1e-3) / 1e12, 2) if bg[1] else None,
+            "gemm_mfma_frac": round(bg[2] / (bg[1] * 1e-3) / PEAK_FP16_MFMA, 4) if bg[1] else None,
+            "attention_ms": round(ba[1], 2),
+            "attention_tflops": round(ba[2] / (ba[1] * 1e-3) / 1e12, 2) if ba[1] else None,
+            "attention_mfma_frac": round(ba[2] / (ba[1] * 1e-3) / PEAK_FP16_MFMA, 4) if ba[1] else None,
+            "z_first": [round(float(x), 4) for x in (zb[0, :, 0] - zb[0, :, 1])],
+        }
+        bmodel.close()
+        del bsynth
+
+    # ---- single Q8_0 matmul, the repo's bench shape: W 3072 x 3072, x 256 x 3072
+    if not args.no_matmul:
+        mr = mc = 3072
+        mt = 256
+        wraw = jev.synth_tensor("bench.matmul.weight", jev.TYPE_Q8_0, mr, mc, 0.02)
+        mx = np.random.default_rng(7).standard_normal((mt, mc)).astype(np.float32)
+        qw = jev.QuantWeight(jev.TYPE_Q8_0, mr, mc, wraw)
+        d_mx = torch.from_numpy(mx).to(dev)
+        d_my = torch.empty((mt, mr), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+        qw.sync()
+        reps = 200
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+        qw.sync()
+        mm_s = (time.perf_counter() - t0) / reps
+        mm_flops = 2.0 * mt * mr * mc
+        my = d_my.cpu().numpy()
+        qw.close()
+        log(f"Q8_0 matmul 256x3072x3072: {mm_s * 1e6:.1f} us/call, {mm_flops / mm_s / 1e12:.1f} TFLOP/s")
+        result["matmul_q8_0"] = {
+            "workload": "W 3072x3072 N(0,0.02) Q8_0, x 256x3072 N(0,1) fp32 (seed 7), y fp32; "
+                        "split + GEMM (+ K-split reduce) per call, back to back",
+            "us_per_call": round(mm_s * 1e6, 2),
+            "tflops": round(mm_flops / mm_s / 1e12, 2),
+            "mfma_frac": round(mm_flops / mm_s / PEAK_FP16_MFMA, 4),
+        }
+        if not args.no_cpu:
+            sys.path.insert(0, ROOT)
+            from oracle import oracle
+            mm_cpu = {}
+            for thr in (1, max(1, min(16, os.cpu_count() or 1))):
+                oracle.set_threads(thr)
+                t0 = time.perf_counter()
+                ref_y = oracle.matmul(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
+                mm_cpu[thr] = mm_flops / (time.perf_counter() - t0) / 1e9
+            err = float(np.max(np.abs(my - ref_y) / np.maximum(1.0, np.abs(ref_y))))
+            result["matmul_q8_0"]["cpu_gflops_by_threads"] = {str(k): round(v, 1) for k, v in mm_cpu.items()}
+            result["matmul_q8_0"]["parity_worst_rel"] = err
+            log(f"CPU oracle matmul: " + ", ".join(f"{k} threads {v:.1f} GFLOP/s" for k, v in mm_cpu.items())
+                + f"; GPU vs CPU worst {err:.2e}")
 
     # ---- CPU baseline: the oracle on the host cores, one 256-token prefill
     if not args.no_cpu:
@@ -212,7 +414,6 @@ def main():
         result["parity_logits_worst_rel"] = err
         ref.close()
 
-    model.close()
     print(json.dumps(result), flush=True)
     return 0
 

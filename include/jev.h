@@ -179,6 +179,22 @@ int jev_profile_enable(jev_ctx *ctx, int enable);
 int jev_profile_read(jev_ctx *ctx, int kernel_class, int64_t *launches, double *total_ms, double *flops,
                      double *bytes);
 
+/* ---- A single quantized weight resident in HBM ---- */
+
+/* The narrower seam QuantMatMul.ForwardAsync(WeightMatrix, x, tokens, y)
+ * (QuantMatMul.cs:66-121) over a weight uploaded once (WeightMatrix.From,
+ * WeightMatrix.cs:53-65: rows = Shape[1], cols = Shape[0], GGUF bytes read
+ * only during the call).  The weight owns its stream and scratch. */
+typedef struct jev_weight jev_weight;
+int jev_weight_create(int ggml_type, int64_t rows, int64_t cols, const void *bytes, size_t nbytes, int device,
+                      jev_weight **out);
+void jev_weight_destroy(jev_weight *w);
+/* y = x . W^T with x [tokens][cols] and y [tokens][rows], both fp32 device
+ * pointers; tokens >= 2 take the MFMA GEMM, 1 token the GEMV (the dispatch of
+ * QuantMatMul.cs:84-101).  Only enqueues on the weight's stream. */
+int jev_matmul_device(jev_weight *w, const float *x, int32_t tokens, float *y);
+int jev_weight_sync(jev_weight *w);
+
 /* ---- Test hooks (no managed counterpart) ---- */
 
 /* Dequantizer.Dequantize (Dequantizer.cs:45-93) run on the device:

@@ -1306,6 +1306,106 @@ int jev_dequantize(int type, const void *src, size_t nbytes, float *dst, int64_t
     return JEV_OK;
 }
 
+struct jev_weight {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    QWeight w;
+    DevBuf<uint16_t> xt;
+    DevBuf<float> xsum, part;
+};
+
+int jev_weight_create(int type, int64_t rows, int64_t cols, const void *bytes, size_t nbytes, int device,
+                      jev_weight **out)
+{
+    if (!out) return fail(JEV_EINVAL, "out is null");
+    *out = nullptr;
+    if (!bytes || rows <= 0 || cols <= 0) return fail(JEV_EINVAL, "bad arguments");
+    if (!is_quant(type) || cols % 32 != 0) return fail(JEV_EINVAL, "unsupported type %d or shape %lld x %lld", type,
+                                                       (long long)rows, (long long)cols);
+    if (nbytes < (size_t)row_bytes(type, cols) * (size_t)rows)
+        return fail(JEV_EDATA, "%zu bytes are too few for a %lld x %lld tensor", nbytes, (long long)rows, (long long)cols);
+    HIP_TRY(hipSetDevice(device));
+    jev_weight *h = new jev_weight;
+    h->device = device;
+    hipError_t e = hipStreamCreate(&h->stream);
+    if (e != hipSuccess) {
+        delete h;
+        return fail(JEV_EDEVICE, "stream: %s", hipGetErrorString(e));
+    }
+    int rc = upload_weight(type, rows, cols, bytes, h->w);
+    if (rc) {
+        (void)hipStreamDestroy(h->stream);
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return JEV_OK;
+}
+
+void jev_weight_destroy(jev_weight *h)
+{
+    if (!h) return;
+    (void)hipSetDevice(h->device);
+    (void)hipStreamSynchronize(h->stream);
+    free_weight(h->w);
+    h->xt.release();
+    h->xsum.release();
+    h->part.release();
+    (void)hipStreamDestroy(h->stream);
+    delete h;
+}
+
+int jev_matmul_device(jev_weight *h, const float *x, int32_t tokens, float *y)
+{
+    if (!h || !x || !y || tokens <= 0) return fail(JEV_EINVAL, "bad arguments");
+    HIP_TRY(hipSetDevice(h->device));
+    const QWeight &w = h->w;
+    const int rows = w.rows, cols = w.cols;
+    const int ksplit = jev_ctx::split(tokens, rows, cols);
+    float *dst = y;
+    if (ksplit > 1) {
+        HIP_TRY(h->part.ensure((size_t)tokens * rows * ksplit));
+        dst = h->part.p;
+    }
+    if (tokens >= 2) {
+        const size_t t16 = ((size_t)tokens + 15) & ~(size_t)15;
+        HIP_TRY(h->xt.ensure(t16 * cols * 2));
+        HIP_TRY(launch_split(x, tokens, cols, h->xt.p, h->stream));
+        if (w.type == kQ5_1) {
+            HIP_TRY(h->xsum.ensure((size_t)tokens * (cols / 32) + 1));
+            HIP_TRY(launch_block_sums(h->xt.p, tokens, cols, h->xsum.p, h->stream));
+        }
+        GemmArgs g;
+        g.M = tokens;
+        g.K = cols;
+        g.xt = h->xt.p;
+        g.xsum = h->xsum.p;
+        g.seg[0] = w;
+        g.ldy = rows;
+        g.y = dst;
+        g.ksplit = ksplit;
+        HIP_TRY(launch_gemm(g, h->stream));
+    } else {
+        GemvArgs g;
+        g.K = cols;
+        g.x = x;
+        g.seg[0] = w;
+        g.y = dst;
+        g.ksplit = ksplit;
+        HIP_TRY(launch_gemv(g, h->stream));
+    }
+    if (ksplit > 1) HIP_TRY(launch_reduce_partials(dst, ksplit, tokens, rows, y, h->stream));
+    return JEV_OK;
+}
+
+int jev_weight_sync(jev_weight *h)
+{
+    if (!h) return fail(JEV_EINVAL, "null weight");
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) return fail(JEV_EDEVICE, "matmul: %s", hipGetErrorString(e));
+    return JEV_OK;
+}
+
 int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const float *x, int32_t tokens, float *y)
 {
     if (!wbytes || !x || !y || tokens <= 0 || rows <= 0 || cols <= 0) return fail(JEV_EINVAL, "bad arguments");

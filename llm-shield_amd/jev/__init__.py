@@ -3,10 +3,11 @@ from ._lib import (ArgumentError, CancelledError, DataError, JevError, OUT_FULL,
                    OUT_SELECTED, TYPE_F16, TYPE_F32, TYPE_NAMES, TYPE_Q4_0, TYPE_Q5_1, TYPE_Q8_0, lib, row_bytes)
 from .model import MINISTRAL_3B, MinistralModel, ModelConfig, TokenLayout, margins
 from .synth import SEED, VERDICT_NO, VERDICT_YES, SynthModel, quantize, random_tokens, synth_tensor
+from .weight import QuantWeight
 
 __all__ = [
     "ArgumentError", "CancelledError", "DataError", "JevError", "MINISTRAL_3B", "MinistralModel", "ModelConfig",
-    "OUT_FULL", "OUT_LAST_FULL", "OUT_NONE", "OUT_SELECTED", "SEED", "SynthModel", "TYPE_F16", "TYPE_F32",
+    "OUT_FULL", "OUT_LAST_FULL", "OUT_NONE", "OUT_SELECTED", "QuantWeight", "SEED", "SynthModel", "TYPE_F16", "TYPE_F32",
     "TYPE_NAMES", "TYPE_Q4_0", "TYPE_Q5_1", "TYPE_Q8_0", "TokenLayout", "VERDICT_NO", "VERDICT_YES", "lib",
     "margins", "quantize", "random_tokens", "row_bytes", "synth_tensor",
 ]

@@ -111,6 +111,10 @@ def lib():
         "jev_profile_enable": (c_int, [c_void_p, c_int]),
         "jev_profile_read": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(ctypes.c_double),
                                      POINTER(ctypes.c_double), POINTER(ctypes.c_double)]),
+        "jev_weight_create": (c_int, [c_int, c_int64, c_int64, c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
+        "jev_weight_destroy": (None, [c_void_p]),
+        "jev_matmul_device": (c_int, [c_void_p, c_void_p, c_int32, c_void_p]),
+        "jev_weight_sync": (c_int, [c_void_p]),
         "jev_dequantize": (c_int, [c_int, c_void_p, c_size_t, F32P, c_int64]),
         "jev_matmul_q": (c_int, [c_int, c_void_p, c_int64, c_int64, F32P, c_int32, F32P]),
         "jev_quantize": (c_int, [c_int, F32P, c_int64, c_void_p, c_size_t]),
@@ -134,5 +138,6 @@ EXPORTED = [
     "jev_last_error", "jev_create", "jev_destroy", "jev_bind_tensor", "jev_finalize", "jev_kv_length",
     "jev_kv_capacity", "jev_kv_reserve", "jev_kv_truncate", "jev_kv_reset", "jev_kv_snapshot", "jev_kv_restore",
     "jev_forward", "jev_forward_tree", "jev_decode_greedy", "jev_margins", "jev_cancel", "jev_forward_device",
-    "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
+    "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
+    "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
 ]
