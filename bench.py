@@ -91,6 +91,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the Q5_1 decode leg")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched Q4_0 decisions leg")
     ap.add_argument("--no-matmul", action="store_true", help="skip the single-matmul leg")
+    ap.add_argument("--decode-once", action="store_true", help="one timed decode run, no warm-up or profiled pass")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy (byte-counter calibration) and exit")
     ap.add_argument("--layers", type=int, default=26, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -100,6 +103,14 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.calib_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 256 MiB")
+        return 0
 
     import jev
     from jev import _lib as L
@@ -261,20 +272,23 @@ def main():
             out = dmodel.decode_greedy(int(prompt[-1]), n_dec)
             return time.perf_counter() - t, out
 
-        decode_run()
+        if not args.decode_once:
+            decode_run()
         dt, toks = decode_run()
         ms_tok = dt / n_dec * 1e3
-        L.check(lib.jev_kv_reset(dh))
-        dmodel.prefill(prompt)
-        L.check(lib.jev_sync(dh))
-        L.check(lib.jev_profile_enable(dh, 1))
-        dmodel.decode_greedy(int(prompt[-1]), n_dec)
-        gv = prof_read(lib, dh, L.PROF_GEMV)
-        da = prof_read(lib, dh, L.PROF_DECODE_ATTN)
-        L.check(lib.jev_profile_enable(dh, 0))
+        gv = da = (0, 0.0, 0.0, 0.0)
+        if not args.decode_once:
+            L.check(lib.jev_kv_reset(dh))
+            dmodel.prefill(prompt)
+            L.check(lib.jev_sync(dh))
+            L.check(lib.jev_profile_enable(dh, 1))
+            dmodel.decode_greedy(int(prompt[-1]), n_dec)
+            gv = prof_read(lib, dh, L.PROF_GEMV)
+            da = prof_read(lib, dh, L.PROF_DECODE_ATTN)
+            L.check(lib.jev_profile_enable(dh, 0))
         gemv_gbs = gv[3] / (gv[1] * 1e-3) / 1e9 if gv[1] else 0.0
         log(f"Q5_1 decode: {ms_tok:.3f} ms/token ({1e3 / ms_tok:.1f} tok/s); GEMV {gemv_gbs:.0f} GB/s "
-            f"({gv[1] / n_dec:.3f} ms/token), attention {da[1] / n_dec:.3f} ms/token")
+            f"({gv[1] / n_dec:.3f} ms/token, event-timed without the graph), attention {da[1] / n_dec:.3f} ms/token")
         result["decode_q5_1"] = {
             "workload": "Q5_1 3B shape, 512-token prefill then 128 greedy decode steps (fp32 KV cache)",
             "ms_per_token": round(ms_tok, 4),
