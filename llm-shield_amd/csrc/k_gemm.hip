@@ -352,15 +352,17 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
                                                                                    p[kk][mi][n], 0, 0, 0);
 #pragma unroll
                 for (int kk = 0; kk < KS; kk++) {
-                    if (k0 + kk == 1 && !second) break; // odd block count: no second block
+                    // an odd block count's missing second block adds 0 * p (p is finite):
+                    // no branch inside the stage's straight-line code
+                    const bool live = k0 + kk == 0 || second;
 #pragma unroll
                     for (int mi = 0; mi < TM; mi++)
 #pragma unroll
                         for (int n = 0; n < NG; n++)
 #pragma unroll
                             for (int r = 0; r < 4; r++) {
-                                float v = fmaf(dsc[kk][n], p[kk][mi][n][r], acc[mi][g * NG + n][r]);
-                                if (TYPE == kQ5_1) v = fmaf(mn[kk][n], f.s[mi][k0 + kk][r], v);
+                                float v = fmaf(live ? dsc[kk][n] : 0.f, p[kk][mi][n][r], acc[mi][g * NG + n][r]);
+                                if (TYPE == kQ5_1) v = fmaf(live ? mn[kk][n] : 0.f, f.s[mi][k0 + kk][r], v);
                                 acc[mi][g * NG + n][r] = v;
                             }
                 }
@@ -591,14 +593,15 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
         const bool second = 2 * st + 1 < nb;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
-            if (bb == 1 && !second) break; // odd block count: no second block
+            // an odd block count's missing second block adds 0 * p (p is finite)
+            const bool live = bb == 0 || second;
             half8_t bf[TN];
             float dv[TN], mv[TN];
 #pragma unroll
             for (int n = 0; n < TN; n++) {
                 bf[n] = decode_b_frag<TYPE>(br[n], bb);
-                dv[n] = h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d));
-                if (TYPE == kQ5_1) mv[n] = h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m));
+                dv[n] = live ? h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d)) : 0.f;
+                if (TYPE == kQ5_1) mv[n] = live ? h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m)) : 0.f;
             }
 #pragma unroll
             for (int mi = 0; mi < TM; mi++) {
