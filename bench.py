@@ -94,6 +94,8 @@ def main():
     ap.add_argument("--decode-once", action="store_true", help="one timed decode run, no warm-up or profiled pass")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (byte-counter calibration) and exit")
+    ap.add_argument("--blas-ref", action="store_true",
+                    help="only time torch.matmul (hipBLASLt) fp16/bf16 on the per-layer prefill shapes and exit")
     ap.add_argument("--layers", type=int, default=26, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -103,6 +105,31 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.blas_ref:
+        # Vendor-library reference: one fp16 (bf16) pass per product, no dequantisation.
+        shapes = [(256, 6144, 3072), (256, 3072, 4096), (256, 18432, 3072), (256, 3072, 9216),
+                  (4528, 6144, 3072), (4528, 18432, 3072)]
+        out = []
+        for (m, n, k) in shapes:
+            for dt in (torch.float16, torch.bfloat16):
+                a = torch.randn(m, k, device="cuda:0", dtype=dt)
+                b = torch.randn(k, n, device="cuda:0", dtype=dt)
+                for _ in range(5):
+                    a @ b
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(50):
+                    a @ b
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) / 50 * 1e3
+                out.append({"m": m, "n": n, "k": k, "dtype": str(dt).split(".")[-1], "us": round(us, 2),
+                            "tflops": round(2.0 * m * n * k / us / 1e6, 1)})
+                log(f"torch.matmul {out[-1]['dtype']} {m}x{n}x{k}: {us:.1f} us, {out[-1]['tflops']} TFLOP/s")
+        print(json.dumps({"blas_reference": out}), flush=True)
+        return 0
 
     if args.calib_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda:0")
@@ -198,6 +225,9 @@ def main():
             "avg_launch_us": round(gemm_avg_ms * 1e3, 2),
             "flops_per_launch": gemm[2] / max(gemm[0], 1),
             "alg_bytes_per_launch": round(gemm[3] / max(gemm[0], 1)),
+            # the fp16 hi/lo activation pair issues two MFMAs per algorithmic one: frac <= 0.5
+            "pair_bound": 0.5,
+            "frac_of_pair_bound": round(gemm_tflops * 1e12 / PEAK_FP16_MFMA / 0.5, 4),
         },
         "breakdown_ms_per_step": {
             "gemm": round(gemm[1] / prof_steps, 4),
