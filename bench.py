@@ -96,6 +96,9 @@ def main():
                     help="only run a 256 MiB device-to-device copy (byte-counter calibration) and exit")
     ap.add_argument("--blas-ref", action="store_true",
                     help="only time torch.matmul (hipBLASLt) fp16/bf16 on the per-layer prefill shapes and exit")
+    ap.add_argument("--gguf-load", action="store_true",
+                    help="only write the synthetic Q8_0 checkpoint as a GGUF file in a temporary directory, "
+                         "time loading it into HBM through the GGUF reader, and exit")
     ap.add_argument("--layers", type=int, default=26, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -146,6 +149,36 @@ def main():
     t0 = time.time()
     synth = jev.SynthModel(cfg, jev.TYPE_Q8_0)
     log(f"synthetic Q8_0 model generated in {time.time() - t0:.1f}s")
+    if args.gguf_load:
+        import shutil
+        import tempfile
+        tmp = tempfile.mkdtemp(prefix="jev-gguf-")
+        try:
+            path = os.path.join(tmp, "synthetic-q8_0.gguf")
+            t0 = time.perf_counter()
+            synth.write_gguf(path)
+            t_write = time.perf_counter() - t0
+            size = os.path.getsize(path)
+            del synth
+            t0 = time.perf_counter()
+            with jev.GgufFile(path) as g:
+                t_parse = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            m = jev.load_gguf(path, initial_kv_capacity=512)
+            L.check(jev.lib().jev_sync(m.handle))
+            t_load = time.perf_counter() - t0
+            tok = jev.random_tokens(16, cfg.vocab, 11)
+            logits = m.forward(tok)
+            m.close()
+            res = {"gguf_load": {"file_bytes": size, "write_s": round(t_write, 3), "parse_s": round(t_parse, 4),
+                                 "load_s": round(t_load, 3), "load_GB_per_s": round(size / t_load / 1e9, 3),
+                                 "finite_logits": bool(np.isfinite(logits).all())}}
+            log(f"GGUF {size / 1e9:.2f} GB: written in {t_write:.1f}s, header parsed in {t_parse * 1e3:.1f} ms, "
+                f"bound to HBM in {t_load:.2f}s ({size / t_load / 1e9:.2f} GB/s)")
+            print(json.dumps(res), flush=True)
+        finally:
+            shutil.rmtree(tmp, ignore_errors=True)
+        return 0
     t0 = time.time()
     model = synth.open(0)
     lib = jev.lib()

@@ -2,11 +2,13 @@
 from ._lib import (ArgumentError, CancelledError, DataError, JevError, OUT_FULL, OUT_LAST_FULL, OUT_NONE,
                    OUT_SELECTED, TYPE_F16, TYPE_F32, TYPE_NAMES, TYPE_Q4_0, TYPE_Q5_1, TYPE_Q8_0, lib, row_bytes)
 from .model import MINISTRAL_3B, MinistralModel, ModelConfig, TokenLayout, margins
+from .gguf import GgufFile, GgufTensorInfo, NotSupportedError, bind_gguf, config_from_gguf, load_gguf, write_gguf
 from .synth import SEED, VERDICT_NO, VERDICT_YES, SynthModel, quantize, random_tokens, synth_tensor
 from .weight import QuantWeight
 
 __all__ = [
-    "ArgumentError", "CancelledError", "DataError", "JevError", "MINISTRAL_3B", "MinistralModel", "ModelConfig",
+    "ArgumentError", "CancelledError", "DataError", "GgufFile", "GgufTensorInfo", "JevError", "NotSupportedError",
+    "bind_gguf", "config_from_gguf", "load_gguf", "write_gguf", "MINISTRAL_3B", "MinistralModel", "ModelConfig",
     "OUT_FULL", "OUT_LAST_FULL", "OUT_NONE", "OUT_SELECTED", "QuantWeight", "SEED", "SynthModel", "TYPE_F16", "TYPE_F32",
     "TYPE_NAMES", "TYPE_Q4_0", "TYPE_Q5_1", "TYPE_Q8_0", "TokenLayout", "VERDICT_NO", "VERDICT_YES", "lib",
     "margins", "quantize", "random_tokens", "row_bytes", "synth_tensor",

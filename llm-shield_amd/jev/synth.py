@@ -88,6 +88,16 @@ class SynthModel:
     def open(self, device: int = 0) -> MinistralModel:
         return self.bind(MinistralModel(self.config, device))
 
+    def write_gguf(self, path: str) -> None:
+        """The checkpoint as a GGUF file with the converter's names and keys; the
+        converter records the quantization type's ggml id as general.file_type."""
+        from .gguf import WriterTensor, ministral_metadata, write_gguf
+        ts = []
+        for name, t in self.tensors.items():
+            shape = (t.cols,) if t.slot in (L.SLOT_OUTPUT_NORM, L.SLOT_ATTN_NORM, L.SLOT_FFN_NORM) else (t.cols, t.rows)
+            ts.append(WriterTensor(name, shape, t.ggml_type, t.data))
+        write_gguf(path, ministral_metadata(self.config, self.ggml_type), ts)
+
 
 def random_tokens(n: int, vocab: int, seed: int) -> np.ndarray:
     """Uniform token ids on [0, vocab)."""

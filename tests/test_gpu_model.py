@@ -207,3 +207,25 @@ def test_finalize_requires_every_tensor(gpu, synth):
     with pytest.raises(jev.DataError):
         m.bind(t.slot, t.layer, t.ggml_type, t.rows, t.cols, t.data[:-1])  # truncated
     m.close()
+
+
+def test_gguf_file_loads_the_same_model_bitwise(gpu, synth, model, tmp_path):
+    """The unchanged loading path: GGUF file -> GgufFile -> jev_bind_tensor from the mapping."""
+    p = tmp_path / "synth.gguf"
+    synth.write_gguf(str(p))
+    toks = jev.random_tokens(45, synth.config.vocab, 21)
+    want = fresh(model).forward(toks)
+    with jev.load_gguf(str(p), initial_kv_capacity=synth.config.initial_kv_capacity) as m:
+        assert m.config.vocab == synth.config.vocab and m.config.n_layers == synth.config.n_layers
+        got = m.forward(toks)
+    assert np.array_equal(got, want)
+
+
+def test_gguf_missing_tensor_is_reported_by_name(gpu, synth, tmp_path):
+    from jev import gguf as G
+    p = tmp_path / "partial.gguf"
+    ts = [G.WriterTensor(n, (t.cols,) if t.rows == 1 else (t.cols, t.rows), t.ggml_type, t.data)
+          for n, t in synth.tensors.items() if n != "blk.1.ffn_up.weight"]
+    G.write_gguf(str(p), G.ministral_metadata(synth.config, synth.ggml_type), ts)
+    with pytest.raises(KeyError, match="blk.1.ffn_up.weight"):
+        jev.load_gguf(str(p))
