@@ -24,6 +24,17 @@ __device__ __forceinline__ void split_f16(float x, uint16_t &hi, uint16_t &lo)
     lo = __builtin_bit_cast(uint16_t, l);
 }
 
+// Two floats as fp16 pairs x = hi + lo, each half rounded toward zero (one
+// v_cvt_pkrtz per part): |x - hi - lo| < 2^-20 |x| for normal fp16 hi.
+__device__ __forceinline__ void split2_rtz(float x0, float x1, uint32_t &hi, uint32_t &lo)
+{
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+    const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(x0 - (float)h[0], x1 - (float)h[1]);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
 // One weight element of the tiled layout, decoded exactly as Dequantizer
 // does (Dequantizer.cs: Q4_0 :155-182, Q5_1 :240-268, Q8_0 :270-305).  d*q is
 // exact in fp32, so the Q5_1 "+ m" rounds once whether or not it is fused.

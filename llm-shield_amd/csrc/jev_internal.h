@@ -170,6 +170,7 @@ struct RopeArgs {
     size_t in_stride = 0;
     float *q_out = nullptr; // [T][qdim]
     float *kc = nullptr, *vc = nullptr; // layer base: [kvh][cap][hd]
+    uint16_t *kp = nullptr, *vp = nullptr; // pair shadows, layer base: [kvh][cap][hi, lo][hd]
     int cap = 0;
     const int32_t *pos = nullptr, *slot = nullptr;
     int start = 0; // used when pos/slot are null (causal append)
@@ -182,7 +183,9 @@ struct RopeArgs {
 hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s);
 
 // Tree-masked attention tiles: consecutive tokens sharing (shared_lo,
-// shared_hi, segment) with consecutive slots, at most 64 per tile.
+// shared_hi, segment) with consecutive slots, at most kAttnTileTokens per tile
+// (the query columns of one 32 x 32 MFMA).
+constexpr int kAttnTileTokens = 32;
 struct AttnTile {
     int32_t t0, n, shared_lo, shared_hi, segment, slot0, pad0, pad1;
 };
@@ -190,7 +193,7 @@ struct AttnArgs {
     int n_tiles = 0, n_heads = 0, group = 4, hd = 128;
     const AttnTile *tiles = nullptr;
     const float *q = nullptr; // [T][qdim]
-    const float *kc = nullptr, *vc = nullptr; // layer base [kvh][cap][hd]
+    const uint16_t *kp = nullptr, *vp = nullptr; // pair shadows, layer base [kvh][cap][hi, lo][hd]
     int cap = 0;
     float scale = 0.f;
     uint16_t *ot = nullptr; // context pair, operand-tile layout, K = qdim
@@ -234,6 +237,9 @@ hipError_t launch_argmax(const float *x, int n, int32_t *result, float *scratch_
                          hipStream_t s);
 
 // KV copy for capacity growth: [L*kvh] heads of `len` rows from stride old_cap to new_cap.
+// Pair shadow of a fp32 cache: [heads_total][cap][hd] -> [heads_total][cap][hi, lo][hd]
+// for positions [0, len).
+hipError_t launch_kv_split(const float *src, uint16_t *dst, int heads_total, int cap, int len, int hd, hipStream_t s);
 hipError_t launch_kv_copy(const float *src, float *dst, int heads_total, int old_cap, int new_cap, int len, int hd,
                           hipStream_t s);
 

@@ -15,17 +15,19 @@
 // depends only on the query's own visible range, never on which other queries
 // share its tile, so a branch scores exactly as it would alone: the tree pass
 // is bit-identical to running the branches one at a time.  Each tile is up to
-// 64 consecutive tokens with one (shared_lo, shared_hi, segment) and
-// consecutive slots; 4 waves take 16 queries each.
+// 32 consecutive tokens with one (shared_lo, shared_hi, segment) and
+// consecutive slots; a workgroup takes one tile and one KV head, and its four
+// waves are four query heads of that KV head, so every staged K/V block
+// serves 4 x 32 query rows.
 //
 // Operands are fp16 pairs (x = hi + lo, ~22 bits): every product is three
-// v_mfma_f32_16x16x32_f16 (hi.hi + hi.lo + lo.hi), which keeps fp32-grade
+// v_mfma_f32_32x32x16_f16 (hi.hi + hi.lo + lo.hi), which keeps fp32-grade
 // scores at a fraction of the fp32-MFMA cost.  The KV cache stays fp32; K and V
 // blocks are split into pairs while being staged in LDS, K as [key][dim] and V
 // transposed to [dim][key] so both operand fragments are vector reads.
 //
-//   S^T (16 keys x 16 queries) = K (16 x 128) . Q^T      12 MFMAs per 16 keys
-//   O^T (128 x 16) += V^T (128 x 64) . P^T (64 x 16)      48 MFMAs per 64 keys,
+//   S^T (32 keys x 32 queries) = K (32 x 128) . Q^T      24 MFMAs per 32 keys
+//   O^T (128 x 32) += V^T (128 x 64) . P^T (64 x 32)      48 MFMAs per 64 keys,
 //                     keys taken in the order the S^T fragments hold them
 //
 // Decode kernel (attn_decode_kernel): few tokens, one query per head, split
@@ -36,9 +38,23 @@
 namespace jev {
 
 namespace {
-constexpr int KB = 64;          // keys per block
-constexpr int KROW = 128 + 8;   // K pair LDS row, halves (padded: conflict-free fragment reads)
-constexpr int VROW = KB + 8;    // transposed V pair LDS row, halves
+constexpr int KB = 64;      // keys per block
+constexpr int KCH = KB * 32; // 16-byte chunks of a staged K or V block: [key][hi, lo][16]
+
+// Chunk swizzle of a staged key row: 16 consecutive keys, and 4 aligned keys
+// x 4 chunks, land on distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int key) { return ((key & 3) << 2) | ((key >> 2) & 3); }
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16 over a 16-lane group: lane 4 a + e receives element e of
+// the 8 bytes addressed by lanes a, a + 4, a + 8, a + 12 (in that order).
+__device__ __forceinline__ uint2 read_tr(const char *p)
+{
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)p);
+    return __builtin_bit_cast(uint2, v);
+}
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
@@ -62,36 +78,75 @@ __device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
 }
 } // namespace
 
-__global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
+__global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t Kh[KB * KROW], Kl[KB * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t Vh[128 * VROW], Vl[128 * VROW];
+    // Double-buffered K and V blocks as fp16 pairs: [key][hi, lo][16 chunks of
+    // 8 dims], chunks swizzled per key (chunk ^ swz(key)) so that both the
+    // K fragment reads and the V transpose reads hit distinct banks.
+    __shared__ __attribute__((aligned(16))) uint4 Ks0[KCH], Vs0[KCH], Ks1[KCH], Vs1[KCH];
 
-    const AttnTile tile = a.tiles[blockIdx.x];
-    const int head = blockIdx.y;
-    const int kvh = head / a.group;
+    // Longest tiles first: the plan lists tiles in token order, and later
+    // tokens see more keys.
+    const AttnTile tile = a.tiles[a.n_tiles - 1 - (int)blockIdx.y];
+    const int hsets = (a.group + 3) >> 2;
+    const int kvh = blockIdx.x / hsets;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4;
+    const int g = lane >> 5, col = lane & 31;
+    const int hl = (blockIdx.x % hsets) * 4 + wave; // query head within the group
+    const bool head_ok = hl < a.group;              // wave-uniform
+    const int head = kvh * a.group + min(hl, a.group - 1);
     const int qdim = a.n_heads * 128;
-    const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
-    const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
+    const char *kpb = (const char *)(a.kp + (size_t)kvh * a.cap * 256);
+    const char *vpb = (const char *)(a.vp + (size_t)kvh * a.cap * 256);
 
     const int n_sh = tile.shared_hi - tile.shared_lo;
-    // This lane's query (column of S^T / O^T).
-    const int qi = 16 * wave + (lane & 15);
-    const bool q_ok = qi < tile.n;
-    const int my_limit = q_ok ? n_sh + (tile.slot0 + qi - tile.segment + 1) : 1;
+    // This lane's query is column `col` of S^T / O^T; lanes col and col + 32
+    // hold the two row halves of it.
+    const bool q_ok = head_ok && col < tile.n;
+    const int my_limit = q_ok ? n_sh + (tile.slot0 + col - tile.segment + 1) : 1;
+    const int min_limit = n_sh + (tile.slot0 - tile.segment + 1); // the tile's first query
     const int max_limit = n_sh + (tile.slot0 + tile.n - 1 - tile.segment + 1);
     const int nblocks = (max_limit + KB - 1) / KB;
+    auto slot_of = [&](int kl) { return kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh); };
 
-    // Q^T fragments: dims 32 c + 8 g .. + 7 of this lane's query, as pairs.
-    half8_t qh[4], ql[4];
-    {
-        const float *qp = a.q + (size_t)(tile.t0 + (q_ok ? qi : 0)) * qdim + head * 128 + 8 * g;
+    // Staging: wave w's load i moves LDS chunks (8 w + i) * 64 + lane, i.e.
+    // key 16 w + 2 i + lane / 32, part (lane / 16) % 2, stored chunk lane % 16;
+    // the lane fetches the logical chunk that position holds.  Keys past the
+    // tile's last visible key are clamped to it: every staged row is a
+    // written cache row (finite), masked for every query, and enters the
+    // context only as 0 * v.
+    int skey[8];
+    uint32_t soff[8];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float4 v0 = q_ok ? *(const float4 *)(qp + 32 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            float4 v1 = q_ok ? *(const float4 *)(qp + 32 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 8; i++) {
+        skey[i] = 16 * wave + 2 * i + (lane >> 5);
+        soff[i] = ((lane >> 4) & 1) * 256 + ((lane & 15) ^ swz(skey[i])) * 16;
+    }
+    auto stage = [&](int b, uint4 *Kd, uint4 *Vd) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int kl = min(b * KB + skey[i], max_limit - 1);
+            const size_t off = (size_t)slot_of(kl) * 512 + soff[i];
+            __builtin_amdgcn_global_load_lds(kpb + off, (__attribute__((address_space(3))) void *)&Kd[(8 * wave + i) * 64],
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vpb + off, (__attribute__((address_space(3))) void *)&Vd[(8 * wave + i) * 64],
+                                             16, 0, 0);
+        }
+    };
+    stage(0, Ks0, Vs0); // in flight while Q is read
+
+    // Q^T fragments: dims 16 c + 8 g .. + 7 of this lane's query, scaled by
+    // 1/sqrt(head_dim) * log2 e (scores come out in log2 units), as pairs.
+    half8_t qh[8], ql[8];
+    {
+        const float sl2 = a.scale * 1.44269504088896340736f;
+        const float *qp = a.q + (size_t)(tile.t0 + (q_ok ? col : 0)) * qdim + head * 128 + 8 * g;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            float4 v0 = q_ok ? *(const float4 *)(qp + 16 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 v1 = q_ok ? *(const float4 *)(qp + 16 * c + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v0 = make_float4(v0.x * sl2, v0.y * sl2, v0.z * sl2, v0.w * sl2);
+            v1 = make_float4(v1.x * sl2, v1.y * sl2, v1.z * sl2, v1.w * sl2);
             uint2 h0, l0, h1, l1;
             split4(v0, h0, l0);
             split4(v1, h1, l1);
@@ -100,165 +155,172 @@ __global__ __launch_bounds__(256, 2) void attn_tree_kernel(AttnArgs a)
         }
     }
 
-    floatx4 o[8];
+    // K fragment of S^T half t, dim chunk c: key 32 t + col, logical chunk
+    // 2 c + g.  swz(32 t + col) = swz(col).
+    uint32_t koff[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    for (int c = 0; c < 8; c++) koff[c] = col * 512 + ((2 * c + g) ^ swz(col)) * 16;
+    // V^T fragment (transpose reads): lane (G = lane / 16, s = lane % 16)
+    // supplies key 16 c + 8 r + 4 (G / 2) + s / 4 at dims 32 d + 16 (G % 2) +
+    // 4 (s % 4); it receives dim 32 d + lane % 32 of the four keys
+    // 16 c + 8 r + 4 (G / 2) + j.  Offsets for c = 0, hi part; c adds 16 keys.
+    uint32_t voff[2][4];
+    {
+        const int s16 = lane & 15, G = lane >> 4, gp = G >> 1;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const int key = 8 * r + 4 * gp + (s16 >> 2);
+                const int lc = 4 * d + 2 * (G & 1) + ((s16 & 3) >> 1);
+                voff[r][d] = key * 512 + ((lc ^ swz(key)) * 16) + 8 * (s16 & 1);
+            }
+    }
 
-    // Staging.  K: thread -> (key tid / 4, quarter row) as pairs in
-    // [key][dim].  V transposed to [dim][key]: thread -> 4 keys (4 (tid % 16)
-    // ..) x 8 dims (8 (tid / 16) ..), so a wave's stores spread over the
-    // banks.  The next block's rows are loaded into registers while the
-    // current block is on the matrix cores; loads are unconditional (the key
-    // clamped, the value zeroed past the end when stored).
-    const int kkey = tid >> 2, kpart = tid & 3;
-    const int vkq = tid & 15, vdq = tid >> 4;
-    float4 kr[8], vr[4][2];
-    auto slot_of = [&](int kl) { return kl < n_sh ? tile.shared_lo + kl : tile.segment + (kl - n_sh); };
-    auto load_kv = [&](int b) __attribute__((always_inline)) {
-        const int kl = min(b * KB + kkey, max_limit - 1);
-        const float4 *ks = (const float4 *)(kbase + (size_t)slot_of(kl) * 128 + kpart * 32);
+    floatx16 o[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) kr[i] = ks[i];
+    for (int d = 0; d < 4; d++)
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int vl = min(b * KB + 4 * vkq + kk, max_limit - 1);
-            const float4 *vs = (const float4 *)(vbase + (size_t)slot_of(vl) * 128 + 8 * vdq);
-            vr[kk][0] = vs[0];
-            vr[kk][1] = vs[1];
-        }
-    };
-    auto store_kv = [&](int b) __attribute__((always_inline)) {
-        {
-            const bool ok = b * KB + kkey < max_limit;
-            uint2 *kh2 = (uint2 *)(Kh + kkey * KROW + kpart * 32);
-            uint2 *kl2 = (uint2 *)(Kl + kkey * KROW + kpart * 32);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                uint2 hv, lv;
-                split4(kr[i], hv, lv);
-                kh2[i] = make_uint2(ok ? hv.x : 0u, ok ? hv.y : 0u);
-                kl2[i] = make_uint2(ok ? lv.x : 0u, ok ? lv.y : 0u);
-            }
-        }
-        {
-            float vv[4][8];
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const bool ok = b * KB + 4 * vkq + kk < max_limit;
-                const float4 v0 = vr[kk][0], v1 = vr[kk][1];
-                vv[kk][0] = ok ? v0.x : 0.f; vv[kk][1] = ok ? v0.y : 0.f;
-                vv[kk][2] = ok ? v0.z : 0.f; vv[kk][3] = ok ? v0.w : 0.f;
-                vv[kk][4] = ok ? v1.x : 0.f; vv[kk][5] = ok ? v1.y : 0.f;
-                vv[kk][6] = ok ? v1.z : 0.f; vv[kk][7] = ok ? v1.w : 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                uint2 hv, lv;
-                split4(make_float4(vv[0][i], vv[1][i], vv[2][i], vv[3][i]), hv, lv);
-                *(uint2 *)(Vh + (8 * vdq + i) * VROW + 4 * vkq) = hv;
-                *(uint2 *)(Vl + (8 * vdq + i) * VROW + 4 * vkq) = lv;
-            }
-        }
-    };
+        for (int j = 0; j < 16; j++) o[d][j] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f; // running max in log2 units
 
-    load_kv(0);
-    for (int b = 0; b < nblocks; b++) {
-        __syncthreads(); // the previous block's fragments have been read
-        store_kv(b);
-        __syncthreads();
-        load_kv(min(b + 1, nblocks - 1)); // in flight during this block's math
+    auto block = [&](int b, const uint4 *Kc, const uint4 *Vc, uint4 *Kn, uint4 *Vn) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's part of block b has landed
+        __syncthreads();                    // everyone's, and block b - 1's buffers are free again
+        if (b + 1 < nblocks) stage(b + 1, Kn, Vn);
+        if (!head_ok) return;
+        const char *kb = (const char *)Kc;
+        const char *vb = (const char *)Vc;
 
-        // S^T for 4 sub-blocks of 16 keys.
-        floatx4 sc[4];
+        // S^T for the block's two 32-key halves, the chains interleaved; the
+        // K fragments of the dim chunk after next are read while this chunk's
+        // six MFMAs run.
+        floatx16 sc[2];
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            floatx4 c = floatx4{0.f, 0.f, 0.f, 0.f};
-            const int row = (16 * s + (lane & 15)) * KROW + 8 * g;
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                half8_t kh = *(const half8_t *)(Kh + row + 32 * cc);
-                half8_t kl = *(const half8_t *)(Kl + row + 32 * cc);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[cc], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[cc], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[cc], c, 0, 0, 0);
+            for (int j = 0; j < 16; j++) sc[t][j] = 0.f;
+        half8_t kf[2][4];
+        auto kread = [&](int c, half8_t (&f)[4]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const char *kr = kb + t * (32 * 512) + koff[c];
+                f[2 * t] = *(const half8_t *)kr;
+                f[2 * t + 1] = *(const half8_t *)(kr + 256);
             }
-            sc[s] = c;
+        };
+        kread(0, kf[0]);
+        kread(1, kf[1]);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const half8_t(&f)[4] = kf[c & 1];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], qh[c], sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], ql[c], sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t + 1], qh[c], sc[t], 0, 0, 0);
+            }
+            if (c + 2 < 8) kread(c + 2, kf[c & 1]);
         }
-        // Scale, mask (by the logical key index), block max.
+        // keep the reads two chunks ahead of the matrix cores
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+            if (c + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        }
+        // Where the block reaches past the tile's first query, mask by the
+        // logical key index; block max.  sc[t][j] holds key
+        // 32 t + 8 (j / 4) + 4 g + j % 4.
+        if ((b + 1) * KB > min_limit) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int kl = b * KB + 32 * t + 8 * (j >> 2) + 4 * g + (j & 3);
+                    sc[t][j] = kl < my_limit ? sc[t][j] : -INFINITY;
+                }
+        }
         float bmax = -INFINITY;
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int kl = b * KB + 16 * s + 4 * g + r;
-                float v = sc[s][r] * a.scale;
-                v = kl < my_limit ? v : -INFINITY;
-                sc[s][r] = v;
-                bmax = fmaxf(bmax, v);
-            }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+            for (int j = 0; j < 16; j++) bmax = fmaxf(bmax, sc[t][j]);
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        float m_new = fmaxf(m_run, bmax);
-        float alpha = __expf(m_run - m_new);
+        const float m_new = fmaxf(m_run, bmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         float psum = 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float p = __expf(sc[s][r] - m_new);
-                sc[s][r] = p;
+            for (int j = 0; j < 16; j++) {
+                const float p = __builtin_amdgcn_exp2f(sc[t][j] - m_new);
+                sc[t][j] = p;
                 psum += p;
             }
-        psum += __shfl_xor(psum, 16, 64);
         psum += __shfl_xor(psum, 32, 64);
         l_run = l_run * alpha + psum;
         m_run = m_new;
+        // o * 1 is o: the rescale runs only when some row's max moved
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+            for (int d = 0; d < 4; d++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) o[j][r] = o[j][r] * alpha;
+                for (int j = 0; j < 16; j++) o[d][j] = o[d][j] * alpha;
+        }
 
-        // O^T += V^T P^T over two 32-key chunks; k slot (g, i) <-> key
-        // 16 (2 c + i / 4) + 4 g + i % 4, the keys this lane's P values hold.
+        // O^T += V^T P^T over four 16-key chunks.  Chunk c's k slot 8 g + i is
+        // key 16 c + 8 (i / 4) + 4 g + i % 4: exactly P values
+        // sc[c / 2][8 (c % 2) + i] of this lane.
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int c = 0; c < 4; c++) {
+            const int t = c >> 1, j0 = 8 * (c & 1);
             uint2 ph0, pl0, ph1, pl1;
-            split4(make_float4(sc[2 * c][0], sc[2 * c][1], sc[2 * c][2], sc[2 * c][3]), ph0, pl0);
-            split4(make_float4(sc[2 * c + 1][0], sc[2 * c + 1][1], sc[2 * c + 1][2], sc[2 * c + 1][3]), ph1, pl1);
-            half8_t bh = cat4(ph0, ph1), bl = cat4(pl0, pl1);
+            split4(make_float4(sc[t][j0], sc[t][j0 + 1], sc[t][j0 + 2], sc[t][j0 + 3]), ph0, pl0);
+            split4(make_float4(sc[t][j0 + 4], sc[t][j0 + 5], sc[t][j0 + 6], sc[t][j0 + 7]), ph1, pl1);
+            const half8_t bh = cat4(ph0, ph1), bl = cat4(pl0, pl1);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int row = (16 * j + (lane & 15)) * VROW + 32 * c + 4 * g;
-                half8_t vh = cat4(*(const uint2 *)(Vh + row), *(const uint2 *)(Vh + row + 16));
-                half8_t vl = cat4(*(const uint2 *)(Vl + row), *(const uint2 *)(Vl + row + 16));
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bh, o[j], 0, 0, 0);
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, bl, o[j], 0, 0, 0);
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, bh, o[j], 0, 0, 0);
+            for (int d = 0; d < 4; d++) {
+                const char *v0 = vb + c * (16 * 512) + voff[0][d];
+                const char *v1 = vb + c * (16 * 512) + voff[1][d];
+                const half8_t vh = cat4(read_tr(v0), read_tr(v1));
+                const half8_t vl = cat4(read_tr(v0 + 256), read_tr(v1 + 256));
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, bh, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, bl, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, bh, o[d], 0, 0, 0);
             }
         }
+    };
+    for (int b = 0; b < nblocks; b += 2) {
+        block(b, Ks0, Vs0, Ks1, Vs1);
+        if (b + 1 < nblocks) block(b + 1, Ks1, Vs1, Ks0, Vs0);
     }
 
     if (q_ok) {
-        // dims 16 j + 4 (lane/16) + r: four consecutive k, one 8-byte store per part
-        float inv = 1.0f / l_run;
-        const int t = tile.t0 + qi, nblk = qdim >> 5;
+        // o[d][j] is dim 32 d + 8 (j / 4) + 4 g + j % 4: four consecutive k, one
+        // 8-byte store per part
+        const float inv = 1.0f / l_run;
+        const int t = tile.t0 + col, nblk = qdim >> 5;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int k = head * 128 + 16 * j + 4 * g;
-            uint2 hv, lv;
-            split4(make_float4(o[j][0] * inv, o[j][1] * inv, o[j][2] * inv, o[j][3] * inv), hv, lv);
-            *(uint2 *)(a.ot + xt_index(t, k, nblk, 0)) = hv;
-            *(uint2 *)(a.ot + xt_index(t, k, nblk, 1)) = lv;
-        }
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+            for (int jq = 0; jq < 4; jq++) {
+                const int k = head * 128 + 32 * d + 8 * jq + 4 * g;
+                uint2 hv, lv;
+                split4(make_float4(o[d][4 * jq] * inv, o[d][4 * jq + 1] * inv, o[d][4 * jq + 2] * inv,
+                                   o[d][4 * jq + 3] * inv), hv, lv);
+                *(uint2 *)(a.ot + xt_index(t, k, nblk, 0)) = hv;
+                *(uint2 *)(a.ot + xt_index(t, k, nblk, 1)) = lv;
+            }
     }
 }
 
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 {
     if (a.n_tiles <= 0) return hipSuccess;
-    if (a.hd != 128) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_tree_kernel, dim3(a.n_tiles, a.n_heads), dim3(256), 0, s, a);
+    if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp) return hipErrorInvalidValue;
+    const int n_kv = a.n_heads / a.group, hsets = (a.group + 3) / 4;
+    hipLaunchKernelGGL(attn_tree_kernel, dim3(n_kv * hsets, a.n_tiles), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

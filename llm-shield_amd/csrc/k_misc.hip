@@ -296,8 +296,17 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
             o0 = m0 - m1;
             o1 = m2 + m3;
         }
-        *(float2 *)(a.kc + ((size_t)h * a.cap + slot) * a.hd + d) = make_float2(o0, o1);
-        *(float2 *)(a.vc + ((size_t)h * a.cap + slot) * a.hd + d) = vv[it];
+        const size_t row = (size_t)h * a.cap + slot;
+        *(float2 *)(a.kc + row * a.hd + d) = make_float2(o0, o1);
+        *(float2 *)(a.vc + row * a.hd + d) = vv[it];
+        // the pair shadows the attention kernel stages from
+        uint32_t hv, lv;
+        split2_rtz(o0, o1, hv, lv);
+        *(uint32_t *)(a.kp + (row * 2 + 0) * a.hd + d) = hv;
+        *(uint32_t *)(a.kp + (row * 2 + 1) * a.hd + d) = lv;
+        split2_rtz(vv[it].x, vv[it].y, hv, lv);
+        *(uint32_t *)(a.vp + (row * 2 + 0) * a.hd + d) = hv;
+        *(uint32_t *)(a.vp + (row * 2 + 1) * a.hd + d) = lv;
         }
     }
 }
@@ -478,6 +487,28 @@ __global__ void kv_copy_kernel(const float *src, float *dst, int old_cap, int ne
     const float *s = src + (size_t)h * old_cap * hd;
     float *d = dst + (size_t)h * new_cap * hd;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) d[i] = s[i];
+}
+
+__global__ void kv_split_kernel(const float *src, uint16_t *dst, int cap, int len, int hd)
+{
+    const int h = blockIdx.y;
+    const size_t n = (size_t)len * hd / 2;
+    const float2 *s = (const float2 *)(src + (size_t)h * cap * hd);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t pos = 2 * i / hd, d = 2 * i % hd, row = (size_t)h * cap + pos;
+        uint32_t hv, lv;
+        split2_rtz(s[i].x, s[i].y, hv, lv);
+        *(uint32_t *)(dst + (row * 2 + 0) * hd + d) = hv;
+        *(uint32_t *)(dst + (row * 2 + 1) * hd + d) = lv;
+    }
+}
+
+hipError_t launch_kv_split(const float *src, uint16_t *dst, int heads_total, int cap, int len, int hd, hipStream_t s)
+{
+    if (len <= 0 || heads_total <= 0) return hipSuccess;
+    if (hd % 2 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kv_split_kernel, dim3(64, heads_total), dim3(256), 0, s, src, dst, cap, len, hd);
+    return hipGetLastError();
 }
 
 hipError_t launch_kv_copy(const float *src, float *dst, int heads_total, int old_cap, int new_cap, int len, int hd,

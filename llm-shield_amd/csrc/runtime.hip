@@ -107,8 +107,11 @@ struct jev_ctx {
     bool finalized = false;
     std::atomic<int> cancel{0};
 
-    // KV arena
+    // KV arena: fp32 K and V (the cache's contents) and their fp16-pair
+    // shadows (same byte size; [layer][kv head][cap][hi, lo][hd]) that the
+    // prefill/tree attention stages from
     float *kc = nullptr, *vc = nullptr;
+    uint16_t *kp = nullptr, *vp = nullptr;
     int cap = 0, len = 0;
 
     // workspace
@@ -293,23 +296,35 @@ int kv_ensure(jev_ctx *c, int required)
     while (cap < required) cap *= 2;
     size_t heads = (size_t)c->cfg.n_layers * c->cfg.n_kv_heads;
     size_t bytes = heads * cap * c->cfg.head_dim * sizeof(float);
-    float *k = nullptr, *v = nullptr;
-    hipError_t e = hipMalloc((void **)&k, bytes);
-    if (e == hipSuccess) e = hipMalloc((void **)&v, bytes);
+    void *buf[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 4 && e == hipSuccess; i++) e = hipMalloc(&buf[i], bytes);
     if (e != hipSuccess) {
-        if (k) (void)hipFree(k);
-        return fail(JEV_ENOMEM, "KV cache growth to %d positions (%zu bytes x 2) failed: %s", cap, bytes,
+        for (void *b : buf)
+            if (b) (void)hipFree(b);
+        return fail(JEV_ENOMEM, "KV cache growth to %d positions (%zu bytes x 4) failed: %s", cap, bytes,
                     hipGetErrorString(e));
     }
+    float *k = (float *)buf[0], *v = (float *)buf[1];
+    uint16_t *kp = (uint16_t *)buf[2], *vp = (uint16_t *)buf[3];
     if (c->kc && c->len > 0) {
+        // a pair row is as long as a fp32 row: the shadows move as 4-byte words
         HIP_TRY(launch_kv_copy(c->kc, k, (int)heads, c->cap, cap, c->len, c->cfg.head_dim, c->stream));
         HIP_TRY(launch_kv_copy(c->vc, v, (int)heads, c->cap, cap, c->len, c->cfg.head_dim, c->stream));
+        HIP_TRY(launch_kv_copy((const float *)c->kp, (float *)kp, (int)heads, c->cap, cap, c->len, c->cfg.head_dim,
+                               c->stream));
+        HIP_TRY(launch_kv_copy((const float *)c->vp, (float *)vp, (int)heads, c->cap, cap, c->len, c->cfg.head_dim,
+                               c->stream));
     }
     HIP_TRY(hipStreamSynchronize(c->stream));
     if (c->kc) (void)hipFree(c->kc);
     if (c->vc) (void)hipFree(c->vc);
+    if (c->kp) (void)hipFree(c->kp);
+    if (c->vp) (void)hipFree(c->vp);
     c->kc = k;
     c->vc = v;
+    c->kp = kp;
+    c->vp = vp;
     c->cap = cap;
     return JEV_OK;
 }
@@ -482,7 +497,7 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
         int s0, lo0, hi0, seg0;
         at(t, s0, lo0, hi0, seg0);
         int n = 1;
-        while (n < 64 && t + n < T) {
+        while (n < kAttnTileTokens && t + n < T) {
             int s, lo, hi, seg;
             at(t + n, s, lo, hi, seg);
             if (lo != lo0 || hi != hi0 || seg != seg0 || s != s0 + n) break;
@@ -555,6 +570,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         const Layer &L = c->layers[l];
         float *kc = c->kc + (size_t)l * c->layer_stride();
         float *vc = c->vc + (size_t)l * c->layer_stride();
+        uint16_t *kp = c->kp + 2 * (size_t)l * c->layer_stride();
+        uint16_t *vp = c->vp + 2 * (size_t)l * c->layer_stride();
 
         // attention norm (+ the previous layer's FFN residual)
         NormArgs na;
@@ -609,6 +626,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.in_stride = (size_t)T * ldqkv;
         ra.q_out = c->q.p;
         ra.kc = kc;
+        ra.kp = kp;
+        ra.vp = vp;
         ra.vc = vc;
         ra.cap = c->cap;
         ra.pos = p.d_pos;
@@ -653,8 +672,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             aa.hd = f.head_dim;
             aa.tiles = c->tiles.p;
             aa.q = c->q.p;
-            aa.kc = kc;
-            aa.vc = vc;
+            aa.kp = kp;
+            aa.vp = vp;
             aa.cap = c->cap;
             aa.scale = scale;
             aa.ot = c->xt.p;
@@ -899,6 +918,8 @@ void jev_destroy(jev_ctx *c)
     if (c->freqs) (void)hipFree(c->freqs);
     if (c->kc) (void)hipFree(c->kc);
     if (c->vc) (void)hipFree(c->vc);
+    if (c->kp) (void)hipFree(c->kp);
+    if (c->vp) (void)hipFree(c->vp);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
     c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->att_ctr.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
@@ -1057,6 +1078,9 @@ int jev_kv_restore(jev_ctx *c, const float *in, size_t n, int32_t length)
                 HIP_TRY(hipMemcpyAsync(dst, in + cur, row * sizeof(float), hipMemcpyHostToDevice, c->stream));
                 cur += row;
             }
+    const int heads = f.n_layers * f.n_kv_heads;
+    HIP_TRY(launch_kv_split(c->kc, c->kp, heads, c->cap, length, f.head_dim, c->stream));
+    HIP_TRY(launch_kv_split(c->vc, c->vp, heads, c->cap, length, f.head_dim, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->len = length;
     return JEV_OK;
