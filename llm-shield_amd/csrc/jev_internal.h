@@ -200,8 +200,9 @@ struct AttnArgs {
 };
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 
-// Decode attention: one query token per entry, split over 64-key chunks,
-// partials combined in chunk order.  ctx fp32 [T][qdim].
+// Decode attention: one query token per entry, split over kDecodeKeys-key
+// chunks, partials combined in chunk order.  ctx fp32 [T][qdim].
+constexpr int kDecodeKeys = 64;
 struct DecodeAttnArgs {
     int T = 0, n_heads = 0, group = 4, hd = 128, max_chunks = 0;
     const float *q = nullptr;

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     const AttnTile tile = a.tiles[a.n_tiles - 1 - (int)blockIdx.y];
     const int hsets = (a.group + 3) >> 2;
     const int kvh = blockIdx.x / hsets;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, col = lane & 31;
     const int hl = (blockIdx.x % hsets) * 4 + wave; // query head within the group
     const bool head_ok = hl < a.group;              // wave-uniform
@@ -120,20 +120,32 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         skey[i] = 16 * wave + 2 * i + (lane >> 5);
-        soff[i] = ((lane >> 4) & 1) * 256 + ((lane & 15) ^ swz(skey[i])) * 16;
+        soff[i] = skey[i] * 512 + ((lane >> 4) & 1) * 256 + ((lane & 15) ^ swz(skey[i])) * 16;
     }
-    auto stage = [&](int b, uint4 *Kd, uint4 *Vd) __attribute__((always_inline)) {
+    // One block of 64 logical keys from `src` into `dst`.  A block inside one
+    // contiguous range below the last visible key has slot = base + key: a
+    // uniform address plus the lane's constant offset.
+    auto stage = [&](int b, const char *src, uint4 *dst) __attribute__((always_inline)) {
+        const int k0 = b * KB;
+        const bool in_shared = k0 + KB <= n_sh, in_seg = k0 >= n_sh;
+        if (k0 + KB <= max_limit && (in_shared || in_seg)) {
+            const int base = (in_shared ? tile.shared_lo + k0 : tile.segment + (k0 - n_sh));
+            const char *sb = src + (size_t)base * 512;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int kl = min(b * KB + skey[i], max_limit - 1);
-            const size_t off = (size_t)slot_of(kl) * 512 + soff[i];
-            __builtin_amdgcn_global_load_lds(kpb + off, (__attribute__((address_space(3))) void *)&Kd[(8 * wave + i) * 64],
-                                             16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vpb + off, (__attribute__((address_space(3))) void *)&Vd[(8 * wave + i) * 64],
-                                             16, 0, 0);
+            for (int i = 0; i < 8; i++)
+                __builtin_amdgcn_global_load_lds(sb + soff[i], (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64],
+                                                 16, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int kl = min(k0 + skey[i], max_limit - 1);
+                const uint32_t off = (uint32_t)slot_of(kl) * 512 + (soff[i] - skey[i] * 512);
+                __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64],
+                                                 16, 0, 0);
+            }
         }
     };
-    stage(0, Ks0, Vs0); // in flight while Q is read
+    stage(0, kpb, Ks0); // in flight while Q is read
 
     // Q^T fragments: dims 16 c + 8 g .. + 7 of this lane's query, scaled by
     // 1/sqrt(head_dim) * log2 e (scores come out in log2 units), as pairs.
@@ -183,54 +195,79 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 #pragma unroll
         for (int j = 0; j < 16; j++) o[d][j] = 0.f;
     float m_run = -INFINITY, l_run = 0.f; // running max in log2 units
+    // P of the previous block as pairs: chunk c's B fragments
+    half8_t pbh[4], pbl[4];
 
-    auto block = [&](int b, const uint4 *Kc, const uint4 *Vc, uint4 *Kn, uint4 *Vn) __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's part of block b has landed
-        __syncthreads();                    // everyone's, and block b - 1's buffers are free again
-        if (b + 1 < nblocks) stage(b + 1, Kn, Vn);
+    // Iteration b: S(b) on the matrix cores, then block b's softmax on the
+    // vector ALUs while block b - 1's P V runs on the matrix cores.  Staged
+    // one iteration ahead: K(b + 1) and V(b).  K and V are double-buffered
+    // (K(b) in Kc, V(b - 1) in Vp; the loads go to Kn and Vn).
+    auto iter = [&](int b, const uint4 *Kc, const uint4 *Vp, uint4 *Kn, uint4 *Vn) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's K(b) and V(b - 1) have landed
+        __syncthreads();                    // everyone's; K(b - 1) and V(b - 2) are free again
+        if (b + 1 < nblocks) stage(b + 1, kpb, Kn);
+        if (b < nblocks) stage(b, vpb, Vn);
         if (!head_ok) return;
-        const char *kb = (const char *)Kc;
-        const char *vb = (const char *)Vc;
+        const bool live = b < nblocks;
 
-        // S^T for the block's two 32-key halves, the chains interleaved; the
-        // K fragments of the dim chunk after next are read while this chunk's
-        // six MFMAs run.
         floatx16 sc[2];
+        if (live) {
+            // S^T for the block's two 32-key halves; the K fragments of the
+            // step after next are read while this step's six MFMAs run.
+            const char *kb = (const char *)Kc;
+            half8_t kf[2][4];
+            auto kread = [&](int c, half8_t (&f)[4]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+                for (int t = 0; t < 2; t++) {
+                    const char *kr = kb + t * (32 * 512) + koff[c];
+                    f[2 * t] = *(const half8_t *)kr;
+                    f[2 * t + 1] = *(const half8_t *)(kr + 256);
+                }
+            };
+            kread(0, kf[0]);
+            kread(1, kf[1]);
 #pragma unroll
-            for (int j = 0; j < 16; j++) sc[t][j] = 0.f;
-        half8_t kf[2][4];
-        auto kread = [&](int c, half8_t (&f)[4]) __attribute__((always_inline)) {
+            for (int c = 0; c < 8; c++) {
+                const half8_t(&f)[4] = kf[c & 1];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const char *kr = kb + t * (32 * 512) + koff[c];
-                f[2 * t] = *(const half8_t *)kr;
-                f[2 * t + 1] = *(const half8_t *)(kr + 256);
+                for (int t = 0; t < 2; t++) {
+                    const floatx16 acc = c == 0 ? floatx16{} : sc[t];
+                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], qh[c], acc, 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], ql[c], sc[t], 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t + 1], qh[c], sc[t], 0, 0, 0);
+                }
+                if (c + 2 < 8) kread(c + 2, kf[c & 1]);
             }
-        };
-        kread(0, kf[0]);
-        kread(1, kf[1]);
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const half8_t(&f)[4] = kf[c & 1];
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], qh[c], sc[t], 0, 0, 0);
-                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], ql[c], sc[t], 0, 0, 0);
-                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t + 1], qh[c], sc[t], 0, 0, 0);
+            for (int c = 0; c < 8; c++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+                if (c + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
             }
-            if (c + 2 < 8) kread(c + 2, kf[c & 1]);
         }
-        // keep the reads two chunks ahead of the matrix cores
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+
+        // O^T += V^T P^T for block b - 1 over four 16-key chunks.  Chunk c's k
+        // slot 8 g + i is key 16 c + 8 (i / 4) + 4 g + i % 4: the P values
+        // sc[c / 2][8 (c % 2) + i] of this lane, split into pbh / pbl.
+        if (b >= 1) {
+            const char *vb = (const char *)Vp;
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
-            if (c + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const char *v0 = vb + c * (16 * 512) + voff[0][d];
+                    const char *v1 = vb + c * (16 * 512) + voff[1][d];
+                    const half8_t vh = cat4(read_tr(v0), read_tr(v1));
+                    const half8_t vl = cat4(read_tr(v0 + 256), read_tr(v1 + 256));
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbl[c], o[d], 0, 0, 0);
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, pbh[c], o[d], 0, 0, 0);
+                }
         }
-        // Where the block reaches past the tile's first query, mask by the
-        // logical key index; block max.  sc[t][j] holds key
+        if (!live) return;
+
+        // Block b's softmax.  Where the block reaches past the tile's first
+        // query, mask by the logical key index.  sc[t][j] holds key
         // 32 t + 8 (j / 4) + 4 g + j % 4.
         if ((b + 1) * KB > min_limit) {
 #pragma unroll
@@ -251,49 +288,35 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         float psum = 0.f;
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int c = 0; c < 4; c++) {
+            const int t = c >> 1, j0 = 8 * (c & 1);
+            float pv[8];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float p = __builtin_amdgcn_exp2f(sc[t][j] - m_new);
-                sc[t][j] = p;
-                psum += p;
+            for (int i = 0; i < 8; i++) {
+                pv[i] = __builtin_amdgcn_exp2f(sc[t][j0 + i] - m_new);
+                psum += pv[i];
             }
+            uint2 ph0, pl0, ph1, pl1;
+            split4(make_float4(pv[0], pv[1], pv[2], pv[3]), ph0, pl0);
+            split4(make_float4(pv[4], pv[5], pv[6], pv[7]), ph1, pl1);
+            pbh[c] = cat4(ph0, ph1);
+            pbl[c] = cat4(pl0, pl1);
+        }
         psum += __shfl_xor(psum, 32, 64);
         l_run = l_run * alpha + psum;
         m_run = m_new;
-        // o * 1 is o: the rescale runs only when some row's max moved
+        // o * 1 is o: the rescale runs only when some row's max moved (after
+        // block b - 1's P V, before block b's)
         if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
             for (int d = 0; d < 4; d++)
 #pragma unroll
                 for (int j = 0; j < 16; j++) o[d][j] = o[d][j] * alpha;
         }
-
-        // O^T += V^T P^T over four 16-key chunks.  Chunk c's k slot 8 g + i is
-        // key 16 c + 8 (i / 4) + 4 g + i % 4: exactly P values
-        // sc[c / 2][8 (c % 2) + i] of this lane.
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int t = c >> 1, j0 = 8 * (c & 1);
-            uint2 ph0, pl0, ph1, pl1;
-            split4(make_float4(sc[t][j0], sc[t][j0 + 1], sc[t][j0 + 2], sc[t][j0 + 3]), ph0, pl0);
-            split4(make_float4(sc[t][j0 + 4], sc[t][j0 + 5], sc[t][j0 + 6], sc[t][j0 + 7]), ph1, pl1);
-            const half8_t bh = cat4(ph0, ph1), bl = cat4(pl0, pl1);
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const char *v0 = vb + c * (16 * 512) + voff[0][d];
-                const char *v1 = vb + c * (16 * 512) + voff[1][d];
-                const half8_t vh = cat4(read_tr(v0), read_tr(v1));
-                const half8_t vl = cat4(read_tr(v0 + 256), read_tr(v1 + 256));
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, bh, o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, bl, o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, bh, o[d], 0, 0, 0);
-            }
-        }
     };
-    for (int b = 0; b < nblocks; b += 2) {
-        block(b, Ks0, Vs0, Ks1, Vs1);
-        if (b + 1 < nblocks) block(b + 1, Ks1, Vs1, Ks0, Vs0);
+    for (int b = 0; b <= nblocks; b += 2) {
+        iter(b, Ks0, Vs1, Ks1, Vs0);
+        if (b + 1 <= nblocks) iter(b + 1, Ks1, Vs0, Ks0, Vs1);
     }
 
     if (q_ok) {
@@ -333,8 +356,9 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 // leaves (max, sum, o[128]) per head; the last workgroup of a (token, KV
 // head) to finish -- counted with an atomic that it resets -- combines the
 // chunks in ascending order, so the result does not depend on timing.
-constexpr int kDecKeys = 64;
+constexpr int kDecKeys = kDecodeKeys;
 constexpr int kDecRow = 132; // padded K row, floats
+constexpr int kDecLoads = kDecKeys * 32 / 256; // float4 loads of K (and of V) per thread
 
 __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 {
@@ -356,16 +380,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
     if (c >= nchunks) return; // this token sees fewer keys
 
-    // ---- stage the chunk's K and V rows (logical key -> cache slot)
+    // ---- this wave's first query head, then the chunk's K and V rows
+    // (logical key -> cache slot), all loads in flight before the first store
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
     const int nk = min(kDecKeys, limit - c * kDecKeys);
+    float q0, q1;
     {
-        // unconditional (clamped) loads, all in flight before the first store
-        float4 kv[8], vv[8];
+        const float *q = a.q + (size_t)t * qdim + (kvh * a.group + min(wave, a.group - 1)) * 128;
+        q0 = q[lane];
+        q1 = q[lane + 64];
+    }
+    {
+        float4 kv[kDecLoads], vv[kDecLoads];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int e = tid + 256 * i; // float4 index in the 64 x 32 chunk
+        for (int i = 0; i < kDecLoads; i++) {
+            const int e = tid + 256 * i; // float4 index in the kDecKeys x 32 chunk
             const int key = min(e >> 5, nk - 1), d4 = e & 31;
             const int kl = c * kDecKeys + key;
             const int p = kl < n_sh ? slo + kl : seg + (kl - n_sh);
@@ -373,7 +403,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
             vv[i] = *(const float4 *)(vbase + (size_t)p * 128 + 4 * d4);
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < kDecLoads; i++) {
             const int e = tid + 256 * i;
             const int key = e >> 5, d4 = e & 31;
             const bool ok = key < nk;
@@ -390,9 +420,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         const bool active = h < a.group;
         const int head = kvh * a.group + min(h, a.group - 1);
         __syncthreads(); // K/V staged; the previous head's qs/ps consumed
-        const float *q = a.q + (size_t)t * qdim + head * 128;
-        qs[wave][lane] = q[lane];
-        qs[wave][lane + 64] = q[lane + 64];
+        if (h0 > 0) {
+            const float *q = a.q + (size_t)t * qdim + head * 128;
+            q0 = q[lane];
+            q1 = q[lane + 64];
+        }
+        qs[wave][lane] = q0;
+        qs[wave][lane + 64] = q1;
         __syncthreads();
         // scores: lane = key
         float sc = -INFINITY;
@@ -413,7 +447,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         const float mx = warp_max(sc);
         const float p = lane < nk ? __expf(sc - mx) : 0.f;
         const float sum = warp_sum(p);
-        ps[wave][lane] = p;
+        if (lane < kDecKeys) ps[wave][lane] = p;
         __syncthreads();
         // weighted sum: lane = dims 2 lane, 2 lane + 1
         float o0 = 0.f, o1 = 0.f;

@@ -511,7 +511,7 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
     }
     p.n_tiles = (int)tiles.size();
     p.kv_rows = std::min<double>(p.end, max_limit + (double)T);
-    p.max_chunks = (max_limit + 63) / 64;
+    p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys;
 
     HIP_TRY(c->ints.ensure(H.size() + 1));
     HIP_TRY(c->tiles.ensure(tiles.size() + 1));
@@ -1194,7 +1194,7 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     Plan p;
     rc = prepare(c, state + 2, true, 1, nullptr, JEV_OUT_LAST_FULL, nullptr, 0, p);
     if (rc) return rc;
-    p.max_chunks = (end + 63) / 64; // grid for the longest step; shorter ones exit early
+    p.max_chunks = (end + kDecodeKeys - 1) / kDecodeKeys; // grid for the longest step; shorter ones exit early
     rc = ensure_workspace(c, 1, p.n_out, JEV_OUT_LAST_FULL, p.max_chunks);
     if (!rc && c->logits.ensure(std::max(c->logits.n, (size_t)c->cfg.vocab)) != hipSuccess) rc = fail(JEV_ENOMEM, "logits");
     if (rc) return rc;
