@@ -22,15 +22,14 @@
 // parallelism, over `ksplit` workgroups whose partials land ksplit * N floats
 // apart (summed in split order by the consumer).  The LM head (many rows)
 // gives each wave its own 16 rows over the whole K instead.  Loads are buffer
-// loads with clamped, branch-free addressing and run a stage of four tiles
-// ahead of the matrix work.
+// loads with clamped, branch-free addressing and run a stage of two or four
+// tiles ahead of the matrix work.
 #include "jev_dev.h"
 
 namespace jev {
 
 namespace {
 
-constexpr int kDepth = 4; // tiles (block pairs) per pipeline stage
 
 // One lane's share of a tile: its quants for both blocks, the two scales /
 // mins of its row and its fifth bits.
@@ -114,8 +113,10 @@ struct TileLoader {
 
 // WR: waves along rows (4: each wave its own 16 rows over the whole range;
 // 1: the four waves share 16 rows and split the range).  Grid: (row groups /
-// WR, ksplit).  nbz: quant blocks per K split (even).
-template <int TYPE, int WR, bool SWIGLU>
+// WR, ksplit).  nbz: quant blocks per K split (even).  DEPTH: tiles (block
+// pairs) per pipeline stage, chosen per shape so that a wave's last stage
+// carries few clamped reloads.
+template <int TYPE, int WR, bool SWIGLU, int DEPTH>
 __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -147,17 +148,17 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
 #pragma unroll
         for (int w = 0; w < NW; w++) ld[w].init(a.seg[SWIGLU ? w : seg], g0, lane);
     }
-    auto load_stage = [&](int st, RawTile (&r)[NW][kDepth]) {
+    auto load_stage = [&](int st, RawTile (&r)[NW][DEPTH]) {
 #pragma unroll
-        for (int j = 0; j < kDepth; j++) {
-            const int kp = kp0 + max(0, min(st * kDepth + j, ntiles - 1)); // clamped: reloads feed no output
+        for (int j = 0; j < DEPTH; j++) {
+            const int kp = kp0 + max(0, min(st * DEPTH + j, ntiles - 1)); // clamped: reloads feed no output
 #pragma unroll
             for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp);
         }
     };
     // the first stage's weights are in flight while x is staged
-    const int nst = (ntiles + kDepth - 1) / kDepth;
-    RawTile r0[NW][kDepth], r1[NW][kDepth];
+    const int nst = (ntiles + DEPTH - 1) / DEPTH;
+    RawTile r0[NW][DEPTH], r1[NW][DEPTH];
     if (nst > 0) load_stage(0, r0);
 
     // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
@@ -206,10 +207,10 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
 #pragma unroll
     for (int w = 0; w < NW; w++) acc[w] = 0.f;
 
-    auto compute_stage = [&](int st, const RawTile (&r)[NW][kDepth]) {
+    auto compute_stage = [&](int st, const RawTile (&r)[NW][DEPTH]) {
 #pragma unroll
-        for (int j = 0; j < kDepth; j++) {
-            const int tl = st * kDepth + j; // tile within the wave's range
+        for (int j = 0; j < DEPTH; j++) {
+            const int tl = st * DEPTH + j; // tile within the wave's range
             const bool valid = tl < ntiles;
             const int lt = t0 + min(tl, ntiles - 1); // tile within the workgroup's range
 #pragma unroll
@@ -281,7 +282,13 @@ static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
     size_t lds = (size_t)nbz * 32 * 2 * 2 + 16 + (size_t)nbz * 4 + 4 * 2 * 16 * 4; // nbz is even
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     dim3 grid(WR == 4 ? (groups + 3) / 4 : groups, a.ksplit);
-    hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU>), grid, dim3(256), lds, s, a, rows, nbz);
+    // tiles of one wave, and the stage depth that pads them least (4 on a tie)
+    const int ntw = nbz / 2, per = WR == 4 ? ntw : (ntw + 3) / 4;
+    const int pad4 = (per + 3) / 4 * 4 - per, pad2 = (per + 1) / 2 * 2 - per;
+    if (pad2 < pad4)
+        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 2>), grid, dim3(256), lds, s, a, rows, nbz);
+    else
+        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 4>), grid, dim3(256), lds, s, a, rows, nbz);
     return hipGetLastError();
 }
 

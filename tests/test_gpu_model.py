@@ -229,3 +229,17 @@ def test_gguf_missing_tensor_is_reported_by_name(gpu, synth, tmp_path):
     G.write_gguf(str(p), G.ministral_metadata(synth.config, synth.ggml_type), ts)
     with pytest.raises(KeyError, match="blk.1.ffn_up.weight"):
         jev.load_gguf(str(p))
+
+
+def test_cache_growth_keeps_the_prefix_bitwise(gpu, synth):
+    """KvCache.EnsureCapacity (KvCache.cs:48-70): growing a populated cache copies its rows (and the
+    pair shadows the tree attention stages from), so continuing after growth equals the whole prompt."""
+    tokens = jev.random_tokens(150, 2048, 12)
+    with synth.bind(jev.MinistralModel(synth.config)) as m:
+        whole = m.forward(tokens)
+    with synth.bind(jev.MinistralModel(synth.config)) as m:
+        assert m.kv_capacity == synth.config.initial_kv_capacity == 64
+        m.prefill(tokens[:60])
+        part = m.forward(tokens[60:])  # 150 positions: 64 -> 128 -> 256
+        assert m.kv_capacity == 256
+    assert np.array_equal(whole, part)
