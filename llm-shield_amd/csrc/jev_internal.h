@@ -213,7 +213,6 @@ struct DecodeAttnArgs {
     const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     float scale = 0.f;
     float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
-    int *counters = nullptr; // [T][n_heads / group], zero between calls
     float *ctx = nullptr;
 };
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);

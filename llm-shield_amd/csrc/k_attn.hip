@@ -32,7 +32,7 @@
 //
 // Decode kernel (attn_decode_kernel): few tokens, one query per head, split
 // over chunks of 64 logical keys per KV head; chunks combined in ascending
-// order by the last workgroup to finish.
+// order by a second, small kernel.
 #include "jev_dev.h"
 
 namespace jev {
@@ -353,9 +353,8 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 // and V rows are staged in LDS once with coalesced loads and serve the
 // group's query heads (wave w takes heads w, w + 4, ...).  Scores: lane =
 // key, fp32 dot over 128 dims; weighted sum: lane = two dims.  Each chunk
-// leaves (max, sum, o[128]) per head; the last workgroup of a (token, KV
-// head) to finish -- counted with an atomic that it resets -- combines the
-// chunks in ascending order, so the result does not depend on timing.
+// leaves (max, sum, o[128]) per head; attn_decode_combine_kernel then sums
+// the chunks in ascending order, so the result does not depend on timing.
 constexpr int kDecKeys = kDecodeKeys;
 constexpr int kDecRow = 132; // padded K row, floats
 constexpr int kDecLoads = kDecKeys * 32 / 256; // float4 loads of K (and of V) per thread
@@ -366,7 +365,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     __shared__ __attribute__((aligned(16))) float Vs[kDecKeys * 128];
     __shared__ __attribute__((aligned(16))) float qs[4][128];
     __shared__ float ps[4][kDecKeys];
-    __shared__ int last;
     const int t = blockIdx.x, kvh = blockIdx.y, c = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qdim = a.n_heads * 128;
@@ -467,62 +465,66 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
             *(float2 *)(part + 2 + 2 * lane) = make_float2(o0, o1);
         }
     }
+}
 
-    // ---- the last chunk of this (token, KV head) to finish combines
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        int *ctr = a.counters + (size_t)t * (a.n_heads / a.group) + kvh;
-        const int done = atomicAdd(ctr, 1);
-        last = done == nchunks - 1;
-        if (last) *ctr = 0; // ready for the next call
+// Chunks of one (token, query head) combined in ascending order.  A kernel of
+// its own: the kernel boundary makes the partials visible, where a
+// last-to-finish combine would need a device-scope fence per workgroup (an L2
+// write-back and invalidate on this multi-XCD part).
+__global__ __launch_bounds__(64) void attn_decode_combine_kernel(DecodeAttnArgs a)
+{
+    const int t = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
+    const int qdim = a.n_heads * 128;
+    const int start = a.start_dev ? *a.start_dev : a.start;
+    const int slot = a.slot ? a.slot[t] : start + t;
+    const int slo = a.shared_lo ? a.shared_lo[t] : 0;
+    const int shi = a.shared_hi ? a.shared_hi[t] : start;
+    const int seg = a.segment ? a.segment[t] : start;
+    const int limit = (shi - slo) + (slot - seg + 1);
+    const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
+    const float *part = a.part + (((size_t)t * a.n_heads) * a.max_chunks + (size_t)head * a.max_chunks) * 130;
+    // eight loads in flight at a time
+    float M = -INFINITY;
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+        float mv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) mv[j] = part[min(c0 + j, nchunks - 1) * 130];
+#pragma unroll
+        for (int j = 0; j < 8; j++) M = fmaxf(M, mv[j]);
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence(); // acquire: the other chunks' partials are visible
-    for (int h = wave; h < a.group; h += 4) {
-        const int head = kvh * a.group + h;
-        const float *part = part_base + (size_t)head * a.max_chunks * 130;
-        // chunks in ascending order, eight loads in flight at a time
-        float M = -INFINITY;
-        for (int c0 = 0; c0 < nchunks; c0 += 8) {
-            float mv[8];
+    float L = 0.f, O0 = 0.f, O1 = 0.f;
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+        float mv[8], lv[8];
+        float2 ov[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) mv[j] = part[min(c0 + j, nchunks - 1) * 130];
-#pragma unroll
-            for (int j = 0; j < 8; j++) M = fmaxf(M, mv[j]);
+        for (int j = 0; j < 8; j++) {
+            const float *pc = part + min(c0 + j, nchunks - 1) * 130;
+            mv[j] = pc[0];
+            lv[j] = pc[1];
+            ov[j] = *(const float2 *)(pc + 2 + 2 * lane);
         }
-        float L = 0.f, O0 = 0.f, O1 = 0.f;
-        for (int c0 = 0; c0 < nchunks; c0 += 8) {
-            float mv[8], lv[8];
-            float2 ov[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float *pc = part + min(c0 + j, nchunks - 1) * 130;
-                mv[j] = pc[0];
-                lv[j] = pc[1];
-                ov[j] = *(const float2 *)(pc + 2 + 2 * lane);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                if (c0 + j < nchunks) {
-                    const float f = __expf(mv[j] - M);
-                    L = fmaf(lv[j], f, L);
-                    O0 = fmaf(ov[j].x, f, O0);
-                    O1 = fmaf(ov[j].y, f, O1);
-                }
+        for (int j = 0; j < 8; j++) {
+            if (c0 + j < nchunks) {
+                const float f = __expf(mv[j] - M);
+                L = fmaf(lv[j], f, L);
+                O0 = fmaf(ov[j].x, f, O0);
+                O1 = fmaf(ov[j].y, f, O1);
             }
         }
-        float *ctx = a.ctx + (size_t)t * qdim + head * 128;
-        *(float2 *)(ctx + 2 * lane) = make_float2(O0 / L, O1 / L);
     }
+    float *ctx = a.ctx + (size_t)t * qdim + head * 128;
+    *(float2 *)(ctx + 2 * lane) = make_float2(O0 / L, O1 / L);
 }
 
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0 || !a.counters) return hipErrorInvalidValue;
+    if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(a.T, a.n_heads), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -315,7 +315,7 @@ hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
     if (a.n_heads * a.hd > 512 * kRopeIters || a.n_kv * a.hd > 512 * kRopeKv || a.nin < 1 || a.nin > kRopeParts ||
-        a.half > 512 || a.hd % 2 != 0)
+        a.half > 512 || a.hd % 2 != 0 || !a.kp || !a.vp)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(rope_store_kernel, dim3(a.T), dim3(256), 0, s, a);
     return hipGetLastError();

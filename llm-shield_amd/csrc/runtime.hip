@@ -118,7 +118,6 @@ struct jev_ctx {
     DevBuf<float> h, y, yo, ydown, q, x32, ctx32, f32, xn, logits, part, xsum;
     DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
     DevBuf<int32_t> ints;
-    DevBuf<int32_t> att_ctr; // decode attention chunk counters (self-resetting, zeroed once)
     DevBuf<AttnTile> tiles;
     DevBuf<float> amax_v;
     DevBuf<int32_t> amax_i;
@@ -386,10 +385,6 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
         HIP_TRY(c->ctx32.ensure((size_t)c->qdim()));
         HIP_TRY(c->f32.ensure((size_t)f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
-        if (c->att_ctr.n < (size_t)f.n_kv_heads) {
-            HIP_TRY(c->att_ctr.ensure((size_t)f.n_kv_heads));
-            HIP_TRY(hipMemset(c->att_ctr.p, 0, c->att_ctr.n * sizeof(int32_t)));
-        }
     } else {
         size_t T16 = ((size_t)T + 15) & ~(size_t)15;
         HIP_TRY(c->xt.ensure(T16 * std::max(f.hidden, c->qdim()) * 2));
@@ -659,7 +654,6 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.start_dev = dpos;
             da.scale = scale;
             da.part = c->part.p;
-            da.counters = c->att_ctr.p;
             da.ctx = c->ctx32.p;
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                          8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
@@ -922,7 +916,7 @@ void jev_destroy(jev_ctx *c)
     if (c->vp) (void)hipFree(c->vp);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
-    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->att_ctr.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
     if (c->copied) (void)hipEventDestroy(c->copied);
