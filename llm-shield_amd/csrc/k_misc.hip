@@ -184,7 +184,9 @@ hipError_t launch_block_sums(const uint16_t *xt, int T, int D, float *xsum, hipS
 // Rope.Apply (Rope.cs:112-135) for q and k of one token, then
 // ApplyPositionScale on q (MinistralModel.cs:676-682); k and v land in their
 // cache slots (StoreKeys / StoreValues, :649-669).  cos/sin are computed in
-// float from position * freq with the accurate library functions.
+// float from position * freq with the accurate library functions.  A token's
+// pairs are shared by gridDim.y workgroups when there are few tokens (every
+// element is independent, so the split changes no result).
 constexpr int kRopeIters = 16; // q pairs per thread: q dims <= 8192
 constexpr int kRopeKv = 4;     // k / v pairs per thread: kv dims <= 2048
 constexpr int kRopeParts = 4;  // K-split partials of the projection
@@ -197,10 +199,15 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
     const int pos = a.pos ? a.pos[t] : start + t;
     const int slot = a.slot ? a.slot[t] : start + t;
     const int qdim = a.n_heads * a.hd, kvdim = a.n_kv * a.hd;
-    const int nq = qdim >> 1, nkv = kvdim >> 1, hpairs = a.hd >> 1;
-    const float2 *qi = (const float2 *)(a.q_in + (size_t)t * a.ld_in);
-    const float2 *ki = (const float2 *)(a.k_in + (size_t)t * a.ld_in);
-    const float2 *vi = (const float2 *)(a.v_in + (size_t)t * a.ld_in);
+    const int nq_all = qdim >> 1, nkv_all = kvdim >> 1, hpairs = a.hd >> 1;
+    // this workgroup's share of the token's q pairs [q0, q0 + nq) and k / v
+    // pairs [k0, k0 + nkv) (gridDim.y workgroups per token)
+    const int qper = (nq_all + gridDim.y - 1) / gridDim.y, kper = (nkv_all + gridDim.y - 1) / gridDim.y;
+    const int q0 = min(nq_all, (int)blockIdx.y * qper), k0 = min(nkv_all, (int)blockIdx.y * kper);
+    const int nq = min(nq_all - q0, qper), nkv = min(nkv_all - k0, kper);
+    const float2 *qi = (const float2 *)(a.q_in + (size_t)t * a.ld_in) + q0;
+    const float2 *ki = (const float2 *)(a.k_in + (size_t)t * a.ld_in) + k0;
+    const float2 *vi = (const float2 *)(a.v_in + (size_t)t * a.ld_in) + k0;
     const size_t zs = a.in_stride >> 1;
     // every load first (clamped indices; lanes past the end drop their value),
     // the K-split partials summed in split order afterwards
@@ -261,12 +268,12 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
             scaled = true;
         }
     }
-    float2 *qo = (float2 *)(a.q_out + (size_t)t * qdim);
+    float2 *qo = (float2 *)(a.q_out + (size_t)t * qdim) + q0;
 #pragma unroll
     for (int it = 0; it < kRopeIters; it++) {
         if (256 * it >= nq) continue;
-        const int p = tid + 256 * it;
-        const int i = p % hpairs;
+        const int p = tid + 256 * it;  // within the share
+        const int i = (q0 + p) % hpairs;
         float x0 = qv[it].x, x1 = qv[it].y;
         float o0 = x0, o1 = x1;
         if (i < a.half) {
@@ -284,10 +291,11 @@ __global__ __launch_bounds__(256) void rope_store_kernel(RopeArgs a)
 #pragma unroll
     for (int it = 0; it < kRopeKv; it++) {
         if (256 * it >= nkv) continue;
-        const int p = tid + 256 * it;
+        const int p = tid + 256 * it; // within the share
         if (p < nkv) {
-        const int i = p % hpairs;
-        const int h = (2 * p) / a.hd, d = (2 * p) % a.hd;
+        const int pg = k0 + p;
+        const int i = pg % hpairs;
+        const int h = (2 * pg) / a.hd, d = (2 * pg) % a.hd;
         float x0 = kv[it].x, x1 = kv[it].y;
         float o0 = x0, o1 = x1;
         if (i < a.half) {
@@ -317,7 +325,9 @@ hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
     if (a.n_heads * a.hd > 512 * kRopeIters || a.n_kv * a.hd > 512 * kRopeKv || a.nin < 1 || a.nin > kRopeParts ||
         a.half > 512 || a.hd % 2 != 0 || !a.kp || !a.vp)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_store_kernel, dim3(a.T), dim3(256), 0, s, a);
+    // few tokens: several workgroups per token share its heads
+    const int split = a.T >= 1024 ? 1 : std::min(8, 1024 / a.T);
+    hipLaunchKernelGGL(rope_store_kernel, dim3(a.T, split), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
