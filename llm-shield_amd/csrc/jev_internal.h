@@ -120,6 +120,9 @@ struct GemvArgs {
     float *y = nullptr;
     int swiglu = 0;
     int ksplit = 1; // K in ksplit ranges (gemm_split_blocks), partial z at y + z * rows
+    // x_up > 0: x holds a gate row and, x_up floats later, an up row; the
+    // input is Kernels.SwiGlu of the pair (silu(g) * u), formed while staging
+    int x_up = 0;
 };
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 // GEMV shape rules, functions of the weight shape only.  Many rows: each wave

@@ -174,6 +174,18 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
             const float4 v0 = xp[0], v1 = xp[1];
             v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
             v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            if (a.x_up > 0) {
+                // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g)
+                const float4 u0 = xp[a.x_up / 4], u1 = xp[a.x_up / 4 + 1];
+                const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float gu = v[j] * u[j];
+                    const float e = expf(-v[j]);
+                    const float sg = 1.0f / (1.0f + e);
+                    v[j] = sg * gu;
+                }
+            }
         }
         uint32_t hw[4], lw[4];
         float bs = 0.f;
@@ -304,7 +316,7 @@ static hipError_t launch_gemv_typed(const GemvArgs &a, hipStream_t s)
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s)
 {
-    if (a.K % 32 != 0 || a.K <= 0 || a.ksplit < 1) return hipErrorInvalidValue;
+    if (a.K % 32 != 0 || a.K <= 0 || a.ksplit < 1 || a.x_up < 0 || a.x_up % 4 != 0) return hipErrorInvalidValue;
     const int nb = a.K >> 5;
     if (a.ksplit > 1 && (a.swiglu || gemm_split_blocks(nb, a.ksplit) * (a.ksplit - 1) >= nb)) return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; i++) {

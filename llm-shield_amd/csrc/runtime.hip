@@ -333,8 +333,9 @@ bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a
 // One linear step y = x . W^T over up to three weights sharing x, as
 // `ksplit` K-split partials T * ldy floats apart.  T >= 2: MFMA GEMM on the
 // fp16 pair in the operand-tile layout; T == 1: GEMV on fp32 x.
+// x_up (one token): x32 holds gate | up rows and the GEMV's input is their SwiGLU.
 int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xt, const float *xsum,
-           const float *x32, float *y, int ldy, int ksplit)
+           const float *x32, float *y, int ldy, int ksplit, int x_up = 0)
 {
     double nrows = 0, wbytes = 0;
     for (int i = 0; i < nw; i++) {
@@ -350,6 +351,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
         for (int i = 0; i < nw; i++) g.seg[i] = *ws[i];
         g.y = y;
         g.ksplit = ksplit;
+        g.x_up = x_up;
         ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows));
         HIP_TRY(launch_gemv(g, c->stream));
         return JEV_OK;
@@ -383,7 +385,7 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
     if (T == 1) {
         HIP_TRY(c->x32.ensure((size_t)std::max<size_t>(f.hidden, 1)));
         HIP_TRY(c->ctx32.ensure((size_t)c->qdim()));
-        HIP_TRY(c->f32.ensure((size_t)f.ffn));
+        HIP_TRY(c->f32.ensure((size_t)2 * f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
     } else {
         size_t T16 = ((size_t)T + 15) & ~(size_t)15;
@@ -692,7 +694,15 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         nf.xsum = (T > 1 && L.gate.type == kQ5_1) ? c->xsum.p : nullptr;
         HIP_TRY(launch_rmsnorm(nf, s));
 
-        if (T == 1) {
+        const bool gu_rows = T == 1 && L.gate.type == L.up.type && f.ffn % 16 == 0;
+        if (gu_rows) {
+            // one token: gate and up rows as one GEMV of 2 x ffn rows (twice the
+            // workgroups of the fused SwiGLU GEMV, so the GPU fills evenly); the
+            // down GEMV forms silu(g) * u while staging its input
+            const QWeight *wgu[2] = {&L.gate, &L.up};
+            int rc = linear(c, T, wgu, 2, nullptr, nullptr, c->x32.p, c->f32.p, 2 * f.ffn, 1);
+            if (rc) return rc;
+        } else if (T == 1) {
             GemvArgs g;
             g.K = D;
             g.x = c->x32.p;
@@ -721,7 +731,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         }
         {
             const QWeight *wd[1] = {&L.down};
-            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down);
+            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
             if (rc) return rc;
         }
     }
