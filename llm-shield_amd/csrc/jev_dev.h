@@ -43,7 +43,7 @@ __device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
     const int rg = row >> 4, r = row & 15, b = k >> 5, kk = k & 31, g = kk >> 3, i = kk & 7, bb = b & 1;
     const int l = 16 * g + r;
     const size_t tile = (size_t)rg * tile_kpairs(w.cols) + (b >> 1);
-    const float d = h2f(w.d[tile * 32 + 2 * r + bb]);
+    const float d = h2f(w.type == kQ5_1 ? w.d[tile * 64 + 4 * r + bb] : w.d[tile * 32 + 2 * r + bb]);
     if (w.type == kQ8_0) {
         const int8_t q = (int8_t)w.qs[tile * 1024 + 16 * l + 8 * bb + i];
         return (float)q * d;
@@ -52,7 +52,7 @@ __device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
     const int nib = i < 4 ? (byte & 15) : (byte >> 4);
     if (w.type == kQ4_0) return d * (float)(nib - 8);
     const int q = nib | (((w.qh[tile * 128 + 2 * l + bb] >> i) & 1) << 4);
-    const float m = h2f(w.m[tile * 32 + 2 * r + bb]);
+    const float m = h2f(w.d[tile * 64 + 4 * r + 2 + bb]);
     const float dq = d * (float)q;
     return dq + m;
 }

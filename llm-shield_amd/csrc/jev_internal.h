@@ -28,8 +28,10 @@ int64_t row_bytes(int type, int64_t cols);
 //   qs  Q8_0       1024 B: lane l's 16 bytes at 16 l -- 8 int8 of block 0, then 8 of block 1
 //       Q4_0/Q5_1   512 B: lane l's 8 bytes at 8 l -- 4 of block 0, then 4 of block 1; byte i
 //                          of a block's four = element 8g+i (low nibble) | element 8g+i+4 (high)
-//   d   fp16         64 B: row r's two block scales at 4 r
-//   m   fp16 (Q5_1)  64 B: as d
+//   d   fp16         64 B: row r's two block scales at 4 r (Q8_0, Q4_0)
+//       Q5_1        128 B: row r's two scales then its two mins at 8 r, so a
+//                          lane's scales and mins are one 8-byte load
+//                          (QWeight::m points at the first min)
 //   qh  (Q5_1)      128 B: lane l's fifth bits at 2 l + block, bit i = element 8 g + i
 constexpr int kTileRows = 16, kTileK = 64;
 struct QWeight {
@@ -46,6 +48,8 @@ struct QWeight {
 __host__ __device__ inline int tile_rows(int rows) { return (rows + kTileRows - 1) / kTileRows; }
 __host__ __device__ inline int tile_kpairs(int cols) { return ((cols >> 5) + 1) >> 1; }
 __host__ __device__ inline int tile_qs_bytes(int type) { return type == kQ8_0 ? 1024 : 512; }
+// Bytes of scales (and Q5_1 mins) per tile.
+__host__ __device__ inline int tile_d_bytes(int type) { return type == kQ5_1 ? 128 : 64; }
 
 // Byte offsets of the fields inside one allocation of the layout above.
 struct QLayout {

@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     // so its weight (segment) is uniform.  Every load is a buffer load: a
     // scalar resource, a per-lane offset fixed for the loop and a scalar
     // per-stage offset; no per-stage vector address arithmetic.
-    rsrc_t rq[CPT], rd[CPT], rm[CPT], rh[CPT];
+    rsrc_t rq[CPT], rd[CPT], rh[CPT];
     int btile0[CPT]; // first tile of the chunk's row group (uniform)
     int b_lds[CPT], b_ds[CPT];
     const int slot = tid & 63, sg = slot >> 4, sr = slot & 15;
@@ -224,11 +224,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
         const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
         rq[j] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
-        rd[j] = make_rsrc(w.d, tiles * 64);
-        if (TYPE == kQ5_1) {
-            rm[j] = make_rsrc(w.m, tiles * 64);
-            rh[j] = make_rsrc(w.qh, tiles * 128);
-        }
+        rd[j] = make_rsrc(w.d, tiles * tile_d_bytes(TYPE));
+        if (TYPE == kQ5_1) rh[j] = make_rsrc(w.qh, tiles * 128);
         // row groups past the weight feed unstored columns
         btile0[j] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + kp_begin);
         b_lds[j] = own ? (16 * t + sr) * LROW + 8 * sg : BN * LROW;
@@ -250,10 +247,14 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
                 uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[j], vq, tile * 512, 0));
                 br[j].q = make_uint4(v.x, v.y, 0u, 0u);
             }
-            br[j].d = __builtin_amdgcn_raw_buffer_load_b32(rd[j], vd, tile * 64, 0);
             if (TYPE == kQ5_1) {
-                br[j].m = __builtin_amdgcn_raw_buffer_load_b32(rm[j], vd, tile * 64, 0);
+                // the row's scales and mins in one load
+                const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[j], 2 * vd, tile * 128, 0));
+                br[j].d = dm.x;
+                br[j].m = dm.y;
                 br[j].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[j], vh, tile * 128, 0);
+            } else {
+                br[j].d = __builtin_amdgcn_raw_buffer_load_b32(rd[j], vd, tile * 64, 0);
             }
         }
     };
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     };
 
     // ---- weight loader: tile n of this wave is tile row wave * TN + n of the workgroup
-    rsrc_t rq[TN], rd[TN], rm[TN], rh[TN];
+    rsrc_t rq[TN], rd[TN], rh[TN];
     int btile0[TN];
     const uint32_t vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
 #pragma unroll
@@ -549,11 +550,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
         const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
         rq[n] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
-        rd[n] = make_rsrc(w.d, tiles * 64);
-        if (TYPE == kQ5_1) {
-            rm[n] = make_rsrc(w.m, tiles * 64);
-            rh[n] = make_rsrc(w.qh, tiles * 128);
-        }
+        rd[n] = make_rsrc(w.d, tiles * tile_d_bytes(TYPE));
+        if (TYPE == kQ5_1) rh[n] = make_rsrc(w.qh, tiles * 128);
         btile0[n] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + (kb_begin >> 1));
     }
     auto load_b = [&](int st, BChunk (&br)[TN]) __attribute__((always_inline)) {
@@ -567,10 +565,13 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
                 uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[n], vq, tile * 512, 0));
                 br[n].q = make_uint4(v.x, v.y, 0u, 0u);
             }
-            br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
             if (TYPE == kQ5_1) {
-                br[n].m = __builtin_amdgcn_raw_buffer_load_b32(rm[n], vd, tile * 64, 0);
+                const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[n], 2 * vd, tile * 128, 0));
+                br[n].d = dm.x;
+                br[n].m = dm.y;
                 br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
+            } else {
+                br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
             }
         }
     };

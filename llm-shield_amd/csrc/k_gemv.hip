@@ -70,7 +70,7 @@ __device__ __forceinline__ float half_of(uint32_t v, int hi) { return h2f((uint1
 // per-lane offsets fixed for the loop, a scalar offset per tile.
 template <int TYPE>
 struct TileLoader {
-    rsrc_t rq, rd, rm, rh;
+    rsrc_t rq, rd, rh;
     uint32_t vq, vd, vh;
     int tile0; // first tile of the row group
 
@@ -79,11 +79,8 @@ struct TileLoader {
         const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
         rq = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
-        rd = make_rsrc(w.d, tiles * 64);
-        if (TYPE == kQ5_1) {
-            rm = make_rsrc(w.m, tiles * 64);
-            rh = make_rsrc(w.qh, tiles * 128);
-        }
+        rd = make_rsrc(w.d, tiles * tile_d_bytes(TYPE));
+        if (TYPE == kQ5_1) rh = make_rsrc(w.qh, tiles * 128);
         vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8);
         vd = 4 * (lane & 15);
         vh = 2 * lane;
@@ -100,10 +97,14 @@ struct TileLoader {
             uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, vq, tile * 512, 0));
             t.q = make_uint4(v.x, v.y, 0u, 0u);
         }
-        t.d = __builtin_amdgcn_raw_buffer_load_b32(rd, vd, tile * 64, 0);
         if (TYPE == kQ5_1) {
-            t.m = __builtin_amdgcn_raw_buffer_load_b32(rm, vd, tile * 64, 0);
+            // the row's scales and mins in one load
+            const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd, 2 * vd, tile * 128, 0));
+            t.d = dm.x;
+            t.m = dm.y;
             t.qh = __builtin_amdgcn_raw_buffer_load_b16(rh, vh, tile * 128, 0);
+        } else {
+            t.d = __builtin_amdgcn_raw_buffer_load_b32(rd, vd, tile * 64, 0);
         }
         return t;
     }

@@ -104,10 +104,10 @@ QLayout qlayout(int type, int64_t rows, int64_t cols)
     const size_t tiles = (size_t)tile_rows((int)rows) * (size_t)tile_kpairs((int)cols);
     l.qs = 0;
     l.d = align256(tiles * tile_qs_bytes(type));
-    size_t end = l.d + tiles * 64;
+    size_t end = l.d + tiles * tile_d_bytes(type);
     if (type == kQ5_1) {
-        l.m = align256(end);
-        l.qh = align256(l.m + tiles * 64);
+        l.m = l.d + 4; // interleaved with the scales: row r's mins at 8 r + 4
+        l.qh = align256(end);
         end = l.qh + tiles * 128;
     }
     l.total = align256(end);
@@ -131,11 +131,8 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
     parallel_rows(RG, threads, [&](int64_t g0, int64_t g1) {
         auto clear = [&](size_t off, size_t per_tile) { std::memset(out + off + g0 * KP * per_tile, 0, (g1 - g0) * KP * per_tile); };
         clear(L.qs, TQ);
-        clear(L.d, 64);
-        if (type == kQ5_1) {
-            clear(L.m, 64);
-            clear(L.qh, 128);
-        }
+        clear(L.d, (size_t)tile_d_bytes(type));
+        if (type == kQ5_1) clear(L.qh, 128);
     });
     parallel_rows(rows, threads, [&](int64_t r0, int64_t r1) {
         for (int64_t row = r0; row < r1; row++) {
@@ -145,7 +142,8 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
                 const uint8_t *blk = rowp + b * ts;
                 const size_t tile = (size_t)(rg * KP + b / 2);
                 const int bb = (int)(b & 1);
-                std::memcpy(out + L.d + tile * 64 + 4 * r + 2 * bb, blk, 2);
+                const size_t dstride = (size_t)tile_d_bytes(type), drow = type == kQ5_1 ? 8 : 4;
+                std::memcpy(out + L.d + tile * dstride + drow * r + 2 * bb, blk, 2);
                 if (type == kQ8_0) {
                     for (int g = 0; g < 4; g++)
                         std::memcpy(out + L.qs + tile * TQ + 16 * (16 * g + r) + 8 * bb, blk + 2 + 8 * g, 8);
@@ -155,7 +153,7 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
                 const uint8_t *qs = blk + (type == kQ4_0 ? 2 : 8);
                 uint32_t qh = 0;
                 if (type == kQ5_1) {
-                    std::memcpy(out + L.m + tile * 64 + 4 * r + 2 * bb, blk + 2, 2);
+                    std::memcpy(out + L.d + tile * dstride + drow * r + 4 + 2 * bb, blk + 2, 2);
                     std::memcpy(&qh, blk + 4, 4);
                 }
                 for (int g = 0; g < 4; g++) {
