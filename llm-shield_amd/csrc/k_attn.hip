@@ -250,19 +250,37 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
         // slot 8 g + i is key 16 c + 8 (i / 4) + 4 g + i % 4: the P values
         // sc[c / 2][8 (c % 2) + i] of this lane, split into pbh / pbl.
         if (b >= 1) {
+            // 16 steps (chunk c, dim tile d); the V^T fragments of the step
+            // after next are read while this step's three MFMAs run
             const char *vb = (const char *)Vp;
+            uint2 vf[3][4];
+            auto vread = [&](int st, uint2 (&f)[4]) __attribute__((always_inline)) {
+                const int c = st >> 2, d = st & 3;
+                const char *v0 = vb + c * (16 * 512) + voff[0][d];
+                const char *v1 = vb + c * (16 * 512) + voff[1][d];
+                f[0] = read_tr(v0);
+                f[1] = read_tr(v1);
+                f[2] = read_tr(v0 + 256);
+                f[3] = read_tr(v1 + 256);
+            };
+            vread(0, vf[0]);
+            vread(1, vf[1]);
 #pragma unroll
-            for (int c = 0; c < 4; c++)
+            for (int st = 0; st < 16; st++) {
+                const int c = st >> 2, d = st & 3;
+                if (st + 2 < 16) vread(st + 2, vf[(st + 2) % 3]);
+                const uint2(&f)[4] = vf[st % 3];
+                const half8_t vh = cat4(f[0], f[1]), vl = cat4(f[2], f[3]);
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbl[c], o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, pbh[c], o[d], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
 #pragma unroll
-                for (int d = 0; d < 4; d++) {
-                    const char *v0 = vb + c * (16 * 512) + voff[0][d];
-                    const char *v1 = vb + c * (16 * 512) + voff[1][d];
-                    const half8_t vh = cat4(read_tr(v0), read_tr(v1));
-                    const half8_t vl = cat4(read_tr(v0 + 256), read_tr(v1 + 256));
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbl[c], o[d], 0, 0, 0);
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, pbh[c], o[d], 0, 0, 0);
-                }
+            for (int st = 0; st < 16; st++) {
+                if (st + 2 < 16) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 1);
+            }
         }
         if (!live) return;
 
