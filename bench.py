@@ -248,7 +248,7 @@ def main():
                    "global_batch": 1, "seq_len": T, "parallelism": "single GPU"},
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_q_kernel (Q8_0)",
+            "kernel": "prefill GEMM launches (gemm_bd_kernel, Q8_0)",
             "achieved": round(gemm_tflops, 2),
             "peak": PEAK_FP16_MFMA / 1e12,
             "unit": "TFLOP/s",

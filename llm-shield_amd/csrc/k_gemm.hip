@@ -26,9 +26,9 @@
 // fragments are loaded straight from global memory (L2-resident) into the
 // MFMA operand registers one stage ahead.  One barrier per stage.
 //
-// Tiles.  4 waves.  Large M: 128 x 128 (waves 4 x 1, each 32 x 128 = 2 x 8
-// MFMA tiles); small M: 64 x 64 (waves 2 x 2, each 32 x 32) for parallelism.
-// Workgroup ids are remapped so each XCD (ids round-robin over 8) works on a
+// Tiles.  4 waves.  This dequant-in-LDS kernel serves segment lists the
+// B-direct kernel below cannot split (64 x 64 tiles at small M, 128 x 128 at
+// large M); the B-direct kernel takes everything else.  Workgroup ids are remapped so each XCD (ids round-robin over 8) works on a
 // contiguous run of a grouped tile order: neighbouring tiles on one XCD share
 // weight and activation tiles in its L2.  LDS rows are padded to 72 halves
 // (144 B) so 16-byte fragment reads of 8 lanes hit distinct banks.
@@ -496,7 +496,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     const int tile_n = (Lp % group) / gsz;
     if (tile_m >= mt || tile_n >= nt) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave-uniform in a scalar register: the activation loads' scalar offset
+    // depends on it, and a vector one would make the compiler wrap each load in
+    // a one-pass loop that drains every outstanding load at the next wait
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = a.M, K = a.K, nblk = K >> 5;
     const int nb_per = gemm_split_blocks(nblk, a.ksplit);
     const int kb_begin = z * nb_per;
@@ -508,21 +511,39 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     // part f & 1) of every row group mi, lane slot tid % 64: 16 bytes each.
     const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
     const rsrc_t ra = make_rsrc(a.xt, (uint32_t)(rg_last + 1) * nblk * 2048);
-    const int af = tid >> 6, abb = af >> 1, apart = af & 1;
+    const int af = wave, abb = af >> 1, apart = af & 1;
     uint32_t va[TM];
 #pragma unroll
     for (int mi = 0; mi < TM; mi++)
         va[mi] = (((uint32_t)min((m0 >> 4) + mi, rg_last) * nblk * 2 + apart) * 512 + lane * 8) * 2;
-    auto load_a = [&](int st, uint4 (&r)[TM]) __attribute__((always_inline)) {
+    // Q5_1 block sums of the stage's BM rows x 2 blocks, one per thread of the
+    // first 2 * BM, staged through LDS with the activations.  The block index
+    // rides in the per-thread offset so the scalar offset stays uniform; the
+    // other threads read past the buffer (zeros).  A missing odd last block
+    // reads a finite neighbour that its zero min cancels.
+    __shared__ __attribute__((aligned(16))) float Xs[2][TYPE == kQ5_1 ? 256 : 4]; // [bb * BM + row], the rest unused
+    rsrc_t rs;
+    uint32_t vx = 0;
+    if (TYPE == kQ5_1) {
+        rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
+        vx = tid < 2 * BM ? ((uint32_t)(m0 + tid % BM) * nblk + tid / BM) * 4 : 0x40000000u;
+    }
+    struct AStage {
+        uint4 v[TM];
+        float xs;
+    };
+    auto load_a = [&](int st, AStage &r) __attribute__((always_inline)) {
         st = min(st, nstage - 1);
         const int kblk = kb_begin + min(2 * st + abb, nb - 1);
 #pragma unroll
         for (int mi = 0; mi < TM; mi++)
-            r[mi] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi], kblk * 2048, 0));
+            r.v[mi] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi], kblk * 2048, 0));
+        if (TYPE == kQ5_1) r.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vx, (kb_begin + 2 * st) * 4, 0));
     };
-    auto store_a = [&](int buf, const uint4 (&r)[TM]) __attribute__((always_inline)) {
+    auto store_a = [&](int buf, const AStage &r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int mi = 0; mi < TM; mi++) *(uint4 *)&As[buf][(mi * 4 + af) * 512 + lane * 8] = r[mi];
+        for (int mi = 0; mi < TM; mi++) *(uint4 *)&As[buf][(mi * 4 + af) * 512 + lane * 8] = r.v[mi];
+        if (TYPE == kQ5_1) Xs[buf][tid] = r.xs;
     };
 
     // ---- weight loader: tile n of this wave is tile row wave * TN + n of the workgroup
@@ -575,14 +596,6 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
             }
         }
     };
-    // Q5_1 block sums of the lane's four C rows
-    rsrc_t rs;
-    uint32_t vs[TM];
-    if (TYPE == kQ5_1) {
-        rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
-#pragma unroll
-        for (int mi = 0; mi < TM; mi++) vs[mi] = (uint32_t)(m0 + mi * 16 + 4 * (lane >> 4)) * nblk * 4;
-    }
 
     floatx4 acc[TM][TN];
 #pragma unroll
@@ -595,26 +608,24 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
             // an odd block count's missing second block adds 0 * p (p is finite)
-            const bool live = bb == 0 || second;
+            // (a mask rather than a select: the compiler turns a select on a
+            // uniform condition into branches around the conversions)
+            const uint32_t live = bb == 0 || second ? ~0u : 0u;
             half8_t bf[TN];
             float dv[TN], mv[TN];
 #pragma unroll
             for (int n = 0; n < TN; n++) {
                 bf[n] = decode_b_frag<TYPE>(br[n], bb);
-                dv[n] = live ? h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d)) : 0.f;
-                if (TYPE == kQ5_1) mv[n] = live ? h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m)) : 0.f;
+                dv[n] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d))) & live);
+                if (TYPE == kQ5_1)
+                    mv[n] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m))) & live);
             }
 #pragma unroll
             for (int mi = 0; mi < TM; mi++) {
                 const half8_t ah = *(const half8_t *)&As[buf][(mi * 4 + bb * 2 + 0) * 512 + lane * 8];
                 const half8_t al = *(const half8_t *)&As[buf][(mi * 4 + bb * 2 + 1) * 512 + lane * 8];
-                floatx4 xs4;
-                if (TYPE == kQ5_1) {
-                    const int kblk = kb_begin + 2 * st + bb;
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        xs4[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vs[mi] + r * nblk * 4, kblk * 4, 0));
-                }
+                floatx4 xs4; // block sums of the lane's four C rows
+                if (TYPE == kQ5_1) xs4 = *(const floatx4 *)&Xs[buf][bb * BM + mi * 16 + 4 * (lane >> 4)];
 #pragma unroll
                 for (int n = 0; n < TN; n++) {
                     floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[n], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -630,24 +641,38 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
         }
     };
 
-    // ---- pipeline: activations one stage ahead through LDS (double
-    // buffered), weights U stages ahead in a register ring.  Whole groups of
-    // U stages in the loop, the remainder after it (see gemm_q_kernel).
+    // ---- pipeline: weights U stages ahead in a register ring; activations
+    // loaded UA stages ahead into a register ring (stage t in slot t % UA)
+    // and copied to LDS (double buffered) by the stage before their own.
+    // Whole groups of U stages in the loop, the remainder after it (see
+    // gemm_q_kernel).  The prologue issues its loads in the loop's order
+    // (activations of stage t + 1, then weights of stage t) so the compiler's
+    // wait counts at the loop head, merged over entry and back edge, stay
+    // those of the loop.
+    // Tall tiles (TM = 4) keep one activation slot: a second would cost the
+    // registers of a third resident workgroup.
+    constexpr int UA = TM >= 4 ? 1 : U;
     BChunk br[U][TN];
-    uint4 araw[TM];
-    load_a(0, araw);
+    AStage araw[UA], a0;
+    load_a(0, a0);
 #pragma unroll
-    for (int j = 0; j < U; j++) load_b(j, br[j]);
-    store_a(0, araw);
-    load_a(1, araw);
+    for (int t = 0; t < U; t++) {
+        if (t < UA) load_a(t + 1, araw[(t + 1) % UA]);
+        load_b(t, br[t]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store_a(0, a0);
     __syncthreads();
     auto stage = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         compute(s, s & 1, br[j]);
-        store_a((s + 1) & 1, araw);
-        load_a(s + 2, araw);
+        store_a((s + 1) & 1, araw[(j + 1) % UA]);
+        load_a(s + 1 + UA, araw[(j + 1) % UA]);
         load_b(s + U, br[j]);
         __syncthreads();
+        // keep the next stage's decode below the barrier: hoisted above it,
+        // it would wait on the weights loaded one stage ago
+        __builtin_amdgcn_sched_barrier(0);
     };
     const int ngroups = nstage / U;
     int s0 = 0;
@@ -767,14 +792,14 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
 #ifdef JEV_GEMM_BD
     return JEV_GEMM_BD(a, s);
 #endif
-    // Measured on MI355X (3B shapes, Q8_0): small batches fill the chip with
-    // 64 x 64 tiles, except the SwiGLU pair, where B-direct 32 x 128 tiles are
-    // faster; large batches take B-direct 64 x 256 tiles.  B-direct needs the
-    // store-mode segments to split on 256-row boundaries.
+    // Measured on MI355X (3B shapes, Q8_0): small batches take B-direct
+    // 32 x 128 tiles (4-5 % ahead of dequant-in-LDS 64 x 64 tiles on the
+    // store shapes), large batches B-direct 64 x 256 tiles.  B-direct needs
+    // the store-mode segments to split on 256-row boundaries.
     bool bd_ok = true;
     for (int i = 0; i + 1 < a.nseg; i++) bd_ok = bd_ok && a.seg[i].rows % 256 == 0;
     if (a.M <= 512) {
-        if (MODE == kGemmSwiGlu) return launch_bd<TYPE, MODE, 2, 2, 1, 4>(a, s);
+        if (MODE == kGemmSwiGlu || bd_ok) return launch_bd<TYPE, MODE, 2, 2, 1, 4>(a, s);
         return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
     }
     if (bd_ok) return launch_bd<TYPE, MODE, 4, 4, 1, 2>(a, s);
