@@ -45,7 +45,7 @@ __device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
     const size_t tile = (size_t)rg * tile_kpairs(w.cols) + (b >> 1);
     const float d = h2f(w.type == kQ5_1 ? w.d[tile * 64 + 4 * r + bb] : w.d[tile * 32 + 2 * r + bb]);
     if (w.type == kQ8_0) {
-        const int8_t q = (int8_t)w.qs[tile * 1024 + 16 * l + 8 * bb + i];
+        const int q = (int)w.qs[tile * 1024 + 16 * l + 8 * bb + i] - 128; // stored biased
         return (float)q * d;
     }
     const uint8_t byte = w.qs[tile * 512 + 8 * l + 4 * bb + (i & 3)];

@@ -25,7 +25,8 @@ int64_t row_bytes(int type, int64_t cols);
 // one wave-wide load of a tile is a single contiguous access.  Tiles are
 // ordered [row group][block pair]; rows pad to a multiple of 16 and blocks to
 // an even count with zero quants and scales.  Per tile:
-//   qs  Q8_0       1024 B: lane l's 16 bytes at 16 l -- 8 int8 of block 0, then 8 of block 1
+//   qs  Q8_0       1024 B: lane l's 16 bytes at 16 l -- 8 quants of block 0, then 8 of block 1,
+//                          each stored biased as the byte q + 128
 //       Q4_0/Q5_1   512 B: lane l's 8 bytes at 8 l -- 4 of block 0, then 4 of block 1; byte i
 //                          of a block's four = element 8g+i (low nibble) | element 8g+i+4 (high)
 //   d   fp16         64 B: row r's two block scales at 4 r (Q8_0, Q4_0)

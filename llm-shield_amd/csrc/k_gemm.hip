@@ -89,8 +89,8 @@ __device__ __forceinline__ half8_t decode_b_frag(const BChunk &c, int bb)
     uint32_t o0, o1, o2, o3;
     if (TYPE == kQ8_0) {
         const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
-        bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
-        bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
+        bytes_to_f16(w0, (_Float16)1152.0f, o0, o1);
+        bytes_to_f16(w1, (_Float16)1152.0f, o2, o3);
     } else {
         const uint32_t w = bb ? c.q.y : c.q.x;
         uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
@@ -116,10 +116,10 @@ __device__ __forceinline__ void store_chunk(const BChunk &c, uint16_t *dst)
     for (int bb = 0; bb < 2; bb++) {
         uint32_t o0, o1, o2, o3;
         if (TYPE == kQ8_0) {
-            // int8 q: bias by 128 (flip the sign bit), then subtract 1152.
+            // stored biased (q + 128): 1024 + byte under the exponent, minus 1152.
             const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
-            bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
-            bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
+            bytes_to_f16(w0, (_Float16)1152.0f, o0, o1);
+            bytes_to_f16(w1, (_Float16)1152.0f, o2, o3);
         } else {
             // byte i = element i (low nibble) | element i + 4 (high nibble)
             const uint32_t w = bb ? c.q.y : c.q.x;

@@ -46,8 +46,8 @@ __device__ __forceinline__ half8_t decode_frag(const RawTile &t, int bb)
     uint32_t o0, o1, o2, o3;
     if (TYPE == kQ8_0) {
         const uint32_t w0 = bb ? t.q.z : t.q.x, w1 = bb ? t.q.w : t.q.y;
-        bytes_to_f16(w0 ^ 0x80808080u, (_Float16)1152.0f, o0, o1);
-        bytes_to_f16(w1 ^ 0x80808080u, (_Float16)1152.0f, o2, o3);
+        bytes_to_f16(w0, (_Float16)1152.0f, o0, o1);
+        bytes_to_f16(w1, (_Float16)1152.0f, o2, o3);
     } else {
         const uint32_t w = bb ? t.q.y : t.q.x;
         uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;

@@ -145,8 +145,12 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
                 const size_t dstride = (size_t)tile_d_bytes(type), drow = type == kQ5_1 ? 8 : 4;
                 std::memcpy(out + L.d + tile * dstride + drow * r + 2 * bb, blk, 2);
                 if (type == kQ8_0) {
-                    for (int g = 0; g < 4; g++)
-                        std::memcpy(out + L.qs + tile * TQ + 16 * (16 * g + r) + 8 * bb, blk + 2 + 8 * g, 8);
+                    // stored biased, q + 128 (the sign bit flipped): the decoders
+                    // place the byte under an fp16 exponent as it is
+                    for (int g = 0; g < 4; g++) {
+                        uint8_t *dq = out + L.qs + tile * TQ + 16 * (16 * g + r) + 8 * bb;
+                        for (int i = 0; i < 8; i++) dq[i] = (uint8_t)(blk[2 + 8 * g + i] ^ 0x80u);
+                    }
                     continue;
                 }
                 // element j of the block: low nibble of byte j (j < 16), high nibble of byte j - 16
