@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int NW = SWIGLU ? 2 : 1; // weights per row (gate and up)
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, rl = lane & 15;
     const int nb = a.K >> 5;
     const int z = blockIdx.y;
@@ -158,12 +158,8 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
         }
     };
     // the first stage's weights are in flight while x is staged
-    // ONE: the wave's whole range is one stage (DEPTH >= its tiles), every
-    // load in flight at once: one memory round trip per wave instead of one
-    // per stage.
-    constexpr bool ONE = DEPTH > 4;
     const int nst = (ntiles + DEPTH - 1) / DEPTH;
-    RawTile r0[NW][DEPTH], r1[NW][ONE ? 1 : DEPTH];
+    RawTile r0[NW][DEPTH], r1[NW][DEPTH];
     if (nst > 0) load_stage(0, r0);
 
     // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
@@ -250,9 +246,7 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
     };
 
     // Two register stages; whole pairs in the loop, the odd stage after it.
-    if constexpr (ONE) {
-        if (nst > 0) compute_stage(0, r0);
-    } else if (nst > 0) {
+    if (nst > 0) {
         int st = 0;
         for (; st + 2 <= nst; st += 2) {
             load_stage(st + 1, r1);
@@ -301,17 +295,10 @@ static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
     size_t lds = (size_t)nbz * 32 * 2 * 2 + 16 + (size_t)nbz * 4 + 4 * 2 * 16 * 4; // nbz is even
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     dim3 grid(WR == 4 ? (groups + 3) / 4 : groups, a.ksplit);
-    // tiles of one wave: up to 12 all in flight at once (one stage of the
-    // next size up), else the stage depth that pads them least (4 on a tie)
+    // tiles of one wave, and the stage depth that pads them least (4 on a tie)
     const int ntw = nbz / 2, per = WR == 4 ? ntw : (ntw + 3) / 4;
     const int pad4 = (per + 3) / 4 * 4 - per, pad2 = (per + 1) / 2 * 2 - per;
-    if (per > 4 && per <= 6)
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 6>), grid, dim3(256), lds, s, a, rows, nbz);
-    else if (per > 6 && per <= 9)
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 9>), grid, dim3(256), lds, s, a, rows, nbz);
-    else if (per > 9 && per <= 12)
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 12>), grid, dim3(256), lds, s, a, rows, nbz);
-    else if (pad2 < pad4)
+    if (pad2 < pad4)
         hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 2>), grid, dim3(256), lds, s, a, rows, nbz);
     else
         hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 4>), grid, dim3(256), lds, s, a, rows, nbz);
