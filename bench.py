@@ -12,7 +12,8 @@ second with the token ids and the model already resident in HBM.  Beside it:
   * 64 independent Q4_0 decisions (512-token trunk + 5 x 32-token branches
     each) evaluated in one tree-masked pass, decisions per second;
   * the repo's single Q8_0 matmul (3072 x 3072 weight, 256 tokens), TFLOP/s,
-    beside the oracle's GFLOP/s on 1 and on all host threads.
+    beside the oracle's GFLOP/s on 1 and on all host threads, and the same
+    call under the opt-in Integer strategy (int8 matrix cores).
 
 Weights are synthetic (N(0, 0.02) quantized with the ggml reference quantizer,
 norms 1.0) because no checkpoint is available offline; token ids are uniform on
@@ -32,6 +33,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "llm-shield_amd"))
 
 PEAK_FP16_MFMA = 2.5e15  # dense fp16 MFMA, MI355X
+PEAK_INT8_MFMA = 5.0e15  # dense int8 MFMA, MI355X
 PEAK_HBM = 8.0e12
 
 
@@ -443,14 +445,35 @@ def main():
         mm_s = (time.perf_counter() - t0) / reps
         mm_flops = 2.0 * mt * mr * mc
         my = d_my.cpu().numpy()
+        # the opt-in Integer strategy on the same call (activation quantization + int8-MFMA block dots)
+        prev = jev.get_matmul_strategy()
+        jev.set_matmul_strategy(jev.MATMUL_INTEGER)
+        try:
+            for _ in range(5):
+                qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+            qw.sync()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+            qw.sync()
+            mi_s = (time.perf_counter() - t0) / reps
+            my_int = d_my.cpu().numpy()
+        finally:
+            jev.set_matmul_strategy(prev)
         qw.close()
-        log(f"Q8_0 matmul 256x3072x3072: {mm_s * 1e6:.1f} us/call, {mm_flops / mm_s / 1e12:.1f} TFLOP/s")
+        log(f"Q8_0 matmul 256x3072x3072: {mm_s * 1e6:.1f} us/call, {mm_flops / mm_s / 1e12:.1f} TFLOP/s; "
+            f"integer strategy {mi_s * 1e6:.1f} us/call, {mm_flops / mi_s / 1e12:.1f} TOP/s")
         result["matmul_q8_0"] = {
             "workload": "W 3072x3072 N(0,0.02) Q8_0, x 256x3072 N(0,1) fp32 (seed 7), y fp32; "
                         "split + GEMM (+ K-split reduce) per call, back to back",
             "us_per_call": round(mm_s * 1e6, 2),
             "tflops": round(mm_flops / mm_s / 1e12, 2),
             "mfma_frac": round(mm_flops / mm_s / PEAK_FP16_MFMA, 4),
+            "integer_strategy": {
+                "us_per_call": round(mi_s * 1e6, 2),
+                "tops": round(mm_flops / mi_s / 1e12, 2),
+                "int8_mfma_frac": round(mm_flops / mi_s / PEAK_INT8_MFMA, 4),
+            },
         }
         if not args.no_cpu:
             sys.path.insert(0, ROOT)
@@ -464,6 +487,12 @@ def main():
             err = float(np.max(np.abs(my - ref_y) / np.maximum(1.0, np.abs(ref_y))))
             result["matmul_q8_0"]["cpu_gflops_by_threads"] = {str(k): round(v, 1) for k, v in mm_cpu.items()}
             result["matmul_q8_0"]["parity_worst_rel"] = err
+            t0 = time.perf_counter()
+            ref_int = oracle.matmul_integer(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
+            mi_cpu = mm_flops / (time.perf_counter() - t0) / 1e9
+            result["matmul_q8_0"]["integer_strategy"]["cpu_gops"] = round(mi_cpu, 1)
+            result["matmul_q8_0"]["integer_strategy"]["bitwise_equal_to_oracle"] = bool(
+                np.array_equal(my_int.view(np.uint32), ref_int.view(np.uint32)))
             log(f"CPU oracle matmul: " + ", ".join(f"{k} threads {v:.1f} GFLOP/s" for k, v in mm_cpu.items())
                 + f"; GPU vs CPU worst {err:.2e}")
 

@@ -195,6 +195,17 @@ void jev_weight_destroy(jev_weight *w);
 int jev_matmul_device(jev_weight *w, const float *x, int32_t tokens, float *y);
 int jev_weight_sync(jev_weight *w);
 
+/* QuantMatMul.Strategy (QuantMatMul.cs:10-41), process-wide, read by every
+ * jev_matmul_device / jev_matmul_q call.  AUTO and FLOAT take the float path
+ * above (exact quants, fp16-pair activations on the fp16 matrix cores: the
+ * numerics the model was validated with); INTEGER is the opt-in integer path
+ * (QuantMatMul.cs:186-287, IntegerDot.cs): activations quantized to Q8_0
+ * blocks, IntegerDot's block dots on the int8 matrix cores.  The model
+ * forward always takes the float path.  JEV_EINVAL for an unknown value. */
+enum { JEV_MATMUL_AUTO = 0, JEV_MATMUL_FLOAT = 1, JEV_MATMUL_INTEGER = 2 };
+int jev_set_matmul_strategy(int strategy);
+int jev_get_matmul_strategy(void);
+
 /* ---- Test hooks (no managed counterpart) ---- */
 
 /* Dequantizer.Dequantize (Dequantizer.cs:45-93) run on the device:
@@ -203,6 +214,12 @@ int jev_dequantize(int ggml_type, const void *src, size_t nbytes, float *dst, in
 /* QuantMatMul.ForwardAsync (QuantMatMul.cs:66-121) run on the device: tokens >= 2
  * take the MFMA GEMM, 1 token the GEMV.  y = tokens x rows. */
 int jev_matmul_q(int ggml_type, const void *w, int64_t rows, int64_t cols, const float *x, int32_t tokens, float *y);
+/* IntegerDot.QuantizeActivations (IntegerDot.cs:60-96) run on the device:
+ * `count` floats (a multiple of 32) to count / 32 Q8_0 blocks of 34 bytes
+ * (Half scale max|x| / 127, quants rounded half away from zero and clamped to
+ * +-127); block_sums (optional, count / 32 floats) gets d * sum(q) with the
+ * float d, as QuantMatMul's integer path computes them (QuantMatMul.cs:223-234). */
+int jev_quantize_activations(const float *x, int64_t count, void *out, size_t out_bytes, float *block_sums);
 
 /* ---- Synthetic-model tool (replaces the converter for offline runs) ---- */
 

@@ -94,6 +94,32 @@ struct GemmArgs {
     int mode = kGemmStore;
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+
+// Integer strategy (IntegerDot): activations x [T][K] fp32 quantized to Q8_0
+// blocks -- int8 quants in int8 MFMA operand tiles (T16 x K bytes), and per
+// (block, token) block-major [K/32][T16]: the Half-rounded scale as float, the
+// integer sum of the quants, and d * sum with the float d.
+struct QuantActArgs {
+    const float *x = nullptr;
+    int T = 0, K = 0, T16 = 0;
+    int8_t *xq = nullptr;
+    float *xd = nullptr;
+    int *xqs = nullptr;
+    float *xs = nullptr;
+};
+hipError_t launch_quant_act(const QuantActArgs &a, hipStream_t s);
+// y [T][ldy] = integer matmul of the quantized activations against w.
+struct GemmI8Args {
+    QWeight w;
+    const int8_t *xq = nullptr;
+    const float *xd = nullptr;
+    const int *xqs = nullptr;
+    const float *xs = nullptr;
+    int T = 0, T16 = 0;
+    float *y = nullptr;
+    int ldy = 0;
+};
+hipError_t launch_gemm_i8(const GemmI8Args &a, hipStream_t s);
 // Quant blocks per K split: an even count (whole 64-wide stages), the last
 // split takes the remainder.  Depends on K and the split count only, so a
 // row's partials are the same whatever M is.

@@ -850,6 +850,9 @@ int prepare(jev_ctx *c, const int32_t *tokens, bool on_device, int T, const jev_
 
 // ================================================================ C ABI
 
+// QuantMatMul.Strategy (QuantMatMul.cs:41): process-wide, read at each call.
+static std::atomic<int> g_matmul_strategy{JEV_MATMUL_AUTO};
+
 extern "C" {
 
 const char *jev_last_error(void) { return g_error.c_str(); }
@@ -1315,6 +1318,68 @@ void jev_cancel(jev_ctx *c)
 
 // ---------------------------------------------------------------- test hooks
 
+int jev_set_matmul_strategy(int strategy)
+{
+    if (strategy != JEV_MATMUL_AUTO && strategy != JEV_MATMUL_FLOAT && strategy != JEV_MATMUL_INTEGER)
+        return fail(JEV_EINVAL, "unknown matmul strategy %d", strategy);
+    g_matmul_strategy.store(strategy);
+    return JEV_OK;
+}
+
+int jev_get_matmul_strategy(void) { return g_matmul_strategy.load(); }
+
+int jev_quantize_activations(const float *x, int64_t count, void *out, size_t out_bytes, float *block_sums)
+{
+    if (!x || !out || count <= 0 || count % 32 != 0) return fail(JEV_EINVAL, "count must be a positive multiple of 32");
+    if (count > (int64_t)1 << 30) return fail(JEV_EINVAL, "count too large");
+    const int64_t nb = count / 32;
+    if (out_bytes < (size_t)nb * 34) return fail(JEV_EINVAL, "output holds %zu bytes, %lld needed", out_bytes,
+                                                 (long long)(nb * 34));
+    // one token of `count` values: the operand tiles hold it in row 0 of a 16-row group
+    float *dx = nullptr, *dd = nullptr, *ds = nullptr;
+    int8_t *dq = nullptr;
+    int *dqs = nullptr;
+    hipError_t e = hipMalloc((void **)&dx, (size_t)count * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&dq, (size_t)count * 16);
+    if (e == hipSuccess) e = hipMalloc((void **)&dd, (size_t)nb * 16 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&ds, (size_t)nb * 16 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&dqs, (size_t)nb * 16 * sizeof(int));
+    if (e == hipSuccess) e = hipMemcpy(dx, x, (size_t)count * sizeof(float), hipMemcpyHostToDevice);
+    std::vector<int8_t> q((size_t)count * 16);
+    std::vector<float> d((size_t)nb * 16), sums((size_t)nb * 16);
+    if (e == hipSuccess) {
+        QuantActArgs a;
+        a.x = dx;
+        a.T = 1;
+        a.K = (int)count;
+        a.T16 = 16;
+        a.xq = dq;
+        a.xd = dd;
+        a.xqs = dqs;
+        a.xs = ds;
+        e = launch_quant_act(a, nullptr);
+    }
+    if (e == hipSuccess) e = hipMemcpy(q.data(), dq, q.size(), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(d.data(), dd, d.size() * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(sums.data(), ds, sums.size() * sizeof(float), hipMemcpyDeviceToHost);
+    for (void *p : {(void *)dx, (void *)dq, (void *)dd, (void *)ds, (void *)dqs})
+        if (p) (void)hipFree(p);
+    if (e != hipSuccess) return fail(JEV_EDEVICE, "quantize activations: %s", hipGetErrorString(e));
+    // reassemble GGUF Q8_0 blocks: Half scale, then the 32 quants of token 0
+    uint8_t *o = (uint8_t *)out;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint16_t h = float_to_half(d[(size_t)b * 16]); // exact: the value is a Half already
+        o[34 * b] = (uint8_t)(h & 0xff);
+        o[34 * b + 1] = (uint8_t)(h >> 8);
+        for (int i = 0; i < 32; i++) {
+            const int k = (int)(32 * b + i), kk = k & 31;
+            o[34 * b + 2 + i] = (uint8_t)q[(((size_t)b * 64) + (kk >> 3) * 16) * 8 + (kk & 7)];
+        }
+        if (block_sums) block_sums[b] = sums[(size_t)b * 16];
+    }
+    return JEV_OK;
+}
+
 int jev_dequantize(int type, const void *src, size_t nbytes, float *dst, int64_t count)
 {
     if (!src || !dst || count <= 0) return fail(JEV_EINVAL, "bad arguments");
@@ -1340,7 +1405,45 @@ struct jev_weight {
     QWeight w;
     DevBuf<uint16_t> xt;
     DevBuf<float> xsum, part;
+    DevBuf<int8_t> xq; // integer strategy: quantized activations and their block data
+    DevBuf<float> xd, xs;
+    DevBuf<int> xqs;
 };
+
+// The Integer strategy on the device: quantize x [tokens][cols] (fp32, device)
+// to Q8_0 blocks, then the int8-MFMA block dots into y [tokens][rows].
+static hipError_t matmul_integer(const QWeight &w, const float *x, int tokens, float *y, DevBuf<int8_t> &xq,
+                                 DevBuf<float> &xd, DevBuf<int> &xqs, DevBuf<float> &xs, hipStream_t s)
+{
+    const int t16 = (tokens + 15) & ~15, nb = w.cols / 32;
+    hipError_t e = xq.ensure((size_t)t16 * w.cols);
+    if (e == hipSuccess) e = xd.ensure((size_t)nb * t16);
+    if (e == hipSuccess) e = xqs.ensure((size_t)nb * t16);
+    if (e == hipSuccess) e = xs.ensure((size_t)nb * t16);
+    if (e != hipSuccess) return e;
+    QuantActArgs q;
+    q.x = x;
+    q.T = tokens;
+    q.K = w.cols;
+    q.T16 = t16;
+    q.xq = xq.p;
+    q.xd = xd.p;
+    q.xqs = xqs.p;
+    q.xs = xs.p;
+    e = launch_quant_act(q, s);
+    if (e != hipSuccess) return e;
+    GemmI8Args g;
+    g.w = w;
+    g.xq = xq.p;
+    g.xd = xd.p;
+    g.xqs = xqs.p;
+    g.xs = xs.p;
+    g.T = tokens;
+    g.T16 = t16;
+    g.y = y;
+    g.ldy = w.rows;
+    return launch_gemm_i8(g, s);
+}
 
 int jev_weight_create(int type, int64_t rows, int64_t cols, const void *bytes, size_t nbytes, int device,
                       jev_weight **out)
@@ -1379,6 +1482,10 @@ void jev_weight_destroy(jev_weight *h)
     h->xt.release();
     h->xsum.release();
     h->part.release();
+    h->xq.release();
+    h->xd.release();
+    h->xs.release();
+    h->xqs.release();
     (void)hipStreamDestroy(h->stream);
     delete h;
 }
@@ -1388,6 +1495,10 @@ int jev_matmul_device(jev_weight *h, const float *x, int32_t tokens, float *y)
     if (!h || !x || !y || tokens <= 0) return fail(JEV_EINVAL, "bad arguments");
     HIP_TRY(hipSetDevice(h->device));
     const QWeight &w = h->w;
+    if (g_matmul_strategy.load() == JEV_MATMUL_INTEGER) {
+        HIP_TRY(matmul_integer(w, x, tokens, y, h->xq, h->xd, h->xqs, h->xs, h->stream));
+        return JEV_OK;
+    }
     const int rows = w.rows, cols = w.cols;
     const int ksplit = jev_ctx::split(tokens, rows, cols);
     float *dst = y;
@@ -1448,7 +1559,17 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
     const int ksplit = jev_ctx::split(tokens, (int)rows, (int)cols);
     if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * ksplit * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
-    if (e == hipSuccess && tokens >= 2) {
+    if (e == hipSuccess && g_matmul_strategy.load() == JEV_MATMUL_INTEGER) {
+        DevBuf<int8_t> xq;
+        DevBuf<float> xd, xs;
+        DevBuf<int> xqs;
+        e = matmul_integer(w, dx, tokens, dy, xq, xd, xqs, xs, nullptr);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        xq.release();
+        xd.release();
+        xs.release();
+        xqs.release();
+    } else if (e == hipSuccess && tokens >= 2) {
         size_t t16 = ((size_t)tokens + 15) & ~(size_t)15;
         e = hipMalloc((void **)&xt, t16 * cols * 2 * sizeof(uint16_t));
         if (e == hipSuccess) e = hipMalloc((void **)&dsum, (nx / 32 + 1) * sizeof(float));

@@ -19,6 +19,8 @@ TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q5_1, TYPE_Q8_0 = 0, 1, 2, 7, 8
  SLOT_FFN_NORM, SLOT_GATE, SLOT_UP, SLOT_DOWN) = range(12)
 OUT_NONE, OUT_LAST_FULL, OUT_SELECTED, OUT_FULL = range(4)
 PROF_GEMM, PROF_ATTN, PROF_GEMV, PROF_DECODE_ATTN = range(4)
+# MatMulStrategy (QuantMatMul.cs:10-18), same numbering
+MATMUL_AUTO, MATMUL_FLOAT, MATMUL_INTEGER = range(3)
 
 TYPE_NAMES = {"F32": TYPE_F32, "F16": TYPE_F16, "Q4_0": TYPE_Q4_0, "Q5_1": TYPE_Q5_1, "Q8_0": TYPE_Q8_0}
 BLOCK = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q4_0: (32, 18), TYPE_Q5_1: (32, 24), TYPE_Q8_0: (32, 34)}
@@ -117,6 +119,9 @@ def lib():
         "jev_weight_sync": (c_int, [c_void_p]),
         "jev_dequantize": (c_int, [c_int, c_void_p, c_size_t, F32P, c_int64]),
         "jev_matmul_q": (c_int, [c_int, c_void_p, c_int64, c_int64, F32P, c_int32, F32P]),
+        "jev_set_matmul_strategy": (c_int, [c_int]),
+        "jev_get_matmul_strategy": (c_int, []),
+        "jev_quantize_activations": (c_int, [F32P, c_int64, c_void_p, c_size_t, F32P]),
         "jev_quantize": (c_int, [c_int, F32P, c_int64, c_void_p, c_size_t]),
         "jev_synth_tensor": (c_int, [c_uint64, c_uint64, c_int, c_int64, c_int64, c_float, c_void_p, c_size_t, c_int]),
     }
@@ -140,4 +145,5 @@ EXPORTED = [
     "jev_forward", "jev_forward_tree", "jev_decode_greedy", "jev_margins", "jev_cancel", "jev_forward_device",
     "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
+    "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations",
 ]

@@ -37,3 +37,26 @@ class QuantWeight:
 
     def sync(self) -> None:
         L.check(self._lib.jev_weight_sync(self._h))
+
+
+def set_matmul_strategy(strategy: int) -> None:
+    """QuantMatMul.Strategy setter (QuantMatMul.cs:41): process-wide, read by
+    every QuantWeight / matmul call; AUTO and FLOAT take the float path,
+    INTEGER the int8 path."""
+    L.check(L.lib().jev_set_matmul_strategy(strategy))
+
+
+def get_matmul_strategy() -> int:
+    return int(L.lib().jev_get_matmul_strategy())
+
+
+def quantize_activations(x: np.ndarray):
+    """IntegerDot.QuantizeActivations on the device: (Q8_0 blocks as uint8,
+    block sums d * sum(q) with the float d)."""
+    xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.empty(xx.size // 32 * 34, np.uint8)
+    sums = np.empty(xx.size // 32, np.float32)
+    F = ctypes.POINTER(ctypes.c_float)
+    L.check(L.lib().jev_quantize_activations(xx.ctypes.data_as(F), xx.size, out.ctypes.data_as(ctypes.c_void_p),
+                                             out.nbytes, sums.ctypes.data_as(F)))
+    return out, sums

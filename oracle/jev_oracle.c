@@ -341,6 +341,149 @@ void orc_matmul(int type, const void *wv, int rows, int cols, const float *x, in
     }
 }
 
+/* ------------------------------------------------------------ integer strategy */
+
+/* binary32 -> binary16, round to nearest even (what the (Half)f conversion
+ * does); used for the stored activation scale. */
+static uint16_t f2h(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds past 65504 */
+    if (ax < 0x38800000u) {                                    /* fp16 subnormal or zero */
+        if (ax < 0x33000000u) return (uint16_t)sign;           /* below half the smallest subnormal */
+        const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+        const int shift = 126 - (int)(ax >> 23);               /* to units of 2^-24 */
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((ax >> 23) - 112) << 10 | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+/* IntegerDot.QuantizeActivations (IntegerDot.cs:60-96), count a multiple of
+ * 32: per block d = max|x| / 127, inverse = d != 0 ? 1 / d : 0, stored scale
+ * (Half)d, q = clamp(round-half-away-from-zero(x * inverse), -127, 127), 34
+ * bytes per block.  `sums` (optional) gets d * sum(q) with the float d, as
+ * QuantMatMul's integer path feeds the Q5_1 offsets (QuantMatMul.cs:223-234). */
+int orc_quantize_activations(const float *x, int64_t count, uint8_t *out, float *sums)
+{
+    if (count % 32 != 0) return -1;
+    for (int64_t b = 0; b < count / 32; b++) {
+        const float *xb = x + 32 * b;
+        uint8_t *o = out + 34 * b;
+        float mx = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            const float a = fabsf(xb[i]);
+            if (a > mx) mx = a;
+        }
+        const float d = mx / 127.0f;
+        const float inverse = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t h = f2h(d);
+        o[0] = (uint8_t)(h & 0xff);
+        o[1] = (uint8_t)(h >> 8);
+        int sum = 0;
+        for (int i = 0; i < 32; i++) {
+            const float scaled = xb[i] * inverse;
+            int v = (int)roundf(scaled);
+            v = v < -127 ? -127 : (v > 127 ? 127 : v);
+            o[2 + i] = (uint8_t)(int8_t)v;
+            sum += v;
+        }
+        if (sums) sums[b] = d * (float)sum;
+    }
+    return 0;
+}
+
+/* IntegerDot.UnpackRow (IntegerDot.cs:113-204) for Q8_0 / Q4_0 / Q5_1: plain
+ * int8 values, per-block scales and (Q5_1) offsets. */
+static void unpack_row(int type, const uint8_t *w, int8_t *v, float *scales, float *offsets, int blocks)
+{
+    for (int b = 0; b < blocks; b++) {
+        if (type == ORC_Q8_0) {
+            const uint8_t *blk = w + 34 * b;
+            scales[b] = h2f(rd16(blk));
+            memcpy(v + 32 * b, blk + 2, 32);
+        } else if (type == ORC_Q4_0) {
+            const uint8_t *blk = w + 18 * b, *qs = blk + 2;
+            scales[b] = h2f(rd16(blk));
+            for (int j = 0; j < 16; j++) {
+                v[32 * b + j] = (int8_t)((qs[j] & 0x0F) - 8);
+                v[32 * b + 16 + j] = (int8_t)((qs[j] >> 4) - 8);
+            }
+        } else { /* Q5_1 */
+            const uint8_t *blk = w + 24 * b, *qs = blk + 8;
+            scales[b] = h2f(rd16(blk));
+            offsets[b] = h2f(rd16(blk + 2));
+            const uint32_t qh = rd32(blk + 4);
+            for (int j = 0; j < 16; j++) {
+                v[32 * b + j] = (int8_t)((qs[j] & 0x0F) | (int)(((qh >> j) & 1) << 4));
+                v[32 * b + 16 + j] = (int8_t)((qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1) << 4));
+            }
+        }
+    }
+}
+
+/* QuantMatMul.ForwardAsync with Strategy = Integer (QuantMatMul.cs:84-100,
+ * ForwardIntegerAsync :186-221, RunRowsInteger :236-287): activations
+ * quantized per token, then per (row, token) the block dots of
+ * IntegerDot.DotPackedQ8_0 / DotUnpacked (IntegerDot.cs:206-272) in their
+ * scalar form -- total += (w_scale * x_scale) * sum(w_i * q_i), blocks
+ * ascending -- plus, for Q5_1, OffsetContribution (:274-279): sum over blocks
+ * of offset * (d * sum(q)), added after the dot.  The AVX2 branches of those
+ * dots keep eight lane partials instead; their order is not pinned by the
+ * reference's tests (IntegerDotTests.cs:56-101 bound the path against the
+ * float one at 1 % relative L2). */
+int orc_matmul_integer(int type, const void *wv, int rows, int cols, const float *x, int tokens, float *y)
+{
+    if ((type != ORC_Q8_0 && type != ORC_Q4_0 && type != ORC_Q5_1) || cols % 32 != 0) return -1;
+    const uint8_t *w = (const uint8_t *)wv;
+    const int blocks = cols / 32;
+    const int64_t rb = orc_row_bytes(type, cols), qrb = (int64_t)blocks * 34;
+    uint8_t *act = (uint8_t *)malloc((size_t)(qrb * tokens));
+    float *sums = (float *)malloc(sizeof(float) * (size_t)blocks * tokens);
+    for (int t = 0; t < tokens; t++) orc_quantize_activations(x + (int64_t)t * cols, cols, act + t * qrb, sums + (int64_t)t * blocks);
+    int nt = orc_get_threads();
+#pragma omp parallel num_threads(nt)
+    {
+        int8_t *v = (int8_t *)malloc((size_t)cols);
+        float *sc = (float *)malloc(sizeof(float) * blocks), *of = (float *)malloc(sizeof(float) * blocks);
+#pragma omp for schedule(static)
+        for (int r = 0; r < rows; r++) {
+            unpack_row(type, w + (int64_t)r * rb, v, sc, of, blocks);
+            for (int t = 0; t < tokens; t++) {
+                const uint8_t *a = act + t * qrb;
+                float total = 0.0f;
+                for (int b = 0; b < blocks; b++) {
+                    const int8_t *q = (const int8_t *)(a + 34 * b + 2);
+                    int sumi = 0;
+                    for (int i = 0; i < 32; i++) sumi += (int)v[32 * b + i] * (int)q[i];
+                    const float s = sc[b] * h2f(rd16(a + 34 * b));
+                    total = total + s * (float)sumi;
+                }
+                if (type == ORC_Q5_1) {
+                    float off = 0.0f;
+                    for (int b = 0; b < blocks; b++) off = off + of[b] * sums[(int64_t)t * blocks + b];
+                    total = total + off;
+                }
+                y[(int64_t)t * rows + r] = total;
+            }
+        }
+        free(v);
+        free(sc);
+        free(of);
+    }
+    free(act);
+    free(sums);
+    return 0;
+}
+
 /* ------------------------------------------------------------ attention */
 
 /* One query against its visible keys: AttentionKernels.Scores (:44-78) gives

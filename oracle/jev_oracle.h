@@ -44,6 +44,12 @@ int orc_dequantize(int type, const void *src, float *dst, int64_t count);
  * row-wise float dot (QuantMatMul.cs:140-176). */
 void orc_matmul(int type, const void *w, int rows, int cols, const float *x, int tokens, float *y);
 
+/* MatMulStrategy.Integer (QuantMatMul.cs:186-287, IntegerDot.cs): Q8_0
+ * activation blocks (34 bytes: Half scale + 32 int8) and the integer matmul.
+ * Both return 0, or -1 for an unsupported type or a count not in whole blocks. */
+int orc_quantize_activations(const float *x, int64_t count, uint8_t *out, float *sums);
+int orc_matmul_integer(int type, const void *w, int rows, int cols, const float *x, int tokens, float *y);
+
 /* Individual kernels (Kernels.cs). */
 void orc_rmsnorm(const float *x, const float *w, float eps, int n, float *y); /* :25-60  */
 void orc_softmax(float *x, int n);                                            /* :102-121 */

@@ -52,6 +52,8 @@ def lib():
         sig = {
             "orc_dequantize": (c_int, [c_int, c_void_p, F, c_int64]),
             "orc_matmul": (None, [c_int, c_void_p, c_int, c_int, F, c_int, F]),
+            "orc_quantize_activations": (c_int, [F, c_int64, c_void_p, F]),
+            "orc_matmul_integer": (c_int, [c_int, c_void_p, c_int, c_int, F, c_int, F]),
             "orc_rmsnorm": (None, [F, F, c_float, c_int, F]),
             "orc_softmax": (None, [F, c_int]),
             "orc_swiglu": (None, [F, F, F, c_int]),
@@ -119,6 +121,26 @@ def matmul(ggml_type: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, t
     y = np.empty(tokens * rows, np.float32)
     wb = np.ascontiguousarray(w).view(np.uint8)
     lib().orc_matmul(ggml_type, wb.ctypes.data_as(c_void_p), rows, cols, fp(xx), tokens, fp(y))
+    return y.reshape(tokens, rows)
+
+
+def quantize_activations(x: np.ndarray):
+    """IntegerDot.QuantizeActivations: (34-byte blocks as uint8, float block sums d * sum(q))."""
+    xx = f32(x).reshape(-1)
+    out = np.empty(xx.size // 32 * 34, np.uint8)
+    sums = np.empty(xx.size // 32, np.float32)
+    if lib().orc_quantize_activations(fp(xx), xx.size, out.ctypes.data_as(c_void_p), fp(sums)) != 0:
+        raise ValueError("count is not whole blocks")
+    return out, sums
+
+
+def matmul_integer(ggml_type: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, tokens: int) -> np.ndarray:
+    """QuantMatMul.ForwardAsync with Strategy = Integer."""
+    xx = f32(x)
+    y = np.empty(tokens * rows, np.float32)
+    wb = np.ascontiguousarray(w).view(np.uint8)
+    if lib().orc_matmul_integer(ggml_type, wb.ctypes.data_as(c_void_p), rows, cols, fp(xx), tokens, fp(y)) != 0:
+        raise ValueError("unsupported type or shape")
     return y.reshape(tokens, rows)
 
 
