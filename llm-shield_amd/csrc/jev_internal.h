@@ -248,6 +248,13 @@ struct DecodeAttnArgs {
     float scale = 0.f;
     float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
     float *ctx = nullptr;
+    // One token (T = 1) with rope_fused: RoPE and the KV store happen here --
+    // q from the projection partials of `rope` (q_in / k_in / v_in, nin,
+    // in_stride, the frequency and scaling fields), the new key and value
+    // written to kc / vc / kp / vp by the workgroup of the chunk that holds
+    // them -- instead of in rope_store_kernel; `q` is then unused.
+    int rope_fused = 0;
+    RopeArgs rope;
 };
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
 

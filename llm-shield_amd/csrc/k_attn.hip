@@ -383,6 +383,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     __shared__ __attribute__((aligned(16))) float Vs[kDecKeys * 128];
     __shared__ __attribute__((aligned(16))) float qs[4][128];
     __shared__ float ps[4][kDecKeys];
+    __shared__ float cs[64], sn[64]; // fused RoPE: cos / sin (times mscale) of the token's position
     const int t = blockIdx.x, kvh = blockIdx.y, c = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qdim = a.n_heads * 128;
@@ -401,12 +402,69 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
     const int nk = min(kDecKeys, limit - c * kDecKeys);
+    // Fused RoPE + KV store (Rope.Apply, Rope.cs:112-135; ApplyPositionScale,
+    // MinistralModel.cs:676-682; StoreKeys / StoreValues :649-669), the same
+    // operations in the same order as rope_store_kernel: the projection's
+    // K-split partials summed in split order, pairs (2i, 2i + 1) rotated by
+    // cos / sin(pos * freq_i) * mscale with separate products, q scaled.
+    const RopeArgs &r = a.rope;
+    const int pos = a.rope_fused ? (r.pos ? r.pos[t] : start + t) : 0;
+    float qscale = 1.f;
+    bool qscaled = false;
+    if (a.rope_fused) {
+        if (tid < r.half) {
+            const float theta = (float)pos * r.freqs[tid];
+            cs[tid] = cosf(theta) * r.mscale;
+            sn[tid] = sinf(theta) * r.mscale;
+        }
+        if (r.orig_ctx > 0 && r.temp_scale != 0.f) {
+            const float interval = floorf((float)pos / (float)r.orig_ctx);
+            if (interval != 0.f) {
+                qscale = 1.f + r.temp_scale * logf(1.f + interval);
+                qscaled = true;
+            }
+        }
+        __syncthreads();
+    }
+    const size_t zs = r.in_stride;
+    // rotated q of one head: this lane holds dims `lane` and `lane + 64`; the
+    // pair partner of dim d is d ^ 1, held by lane ^ 1
+    auto rope_q = [&](int head, float &o0, float &o1) __attribute__((always_inline)) {
+        const float *qi = r.q_in + (size_t)t * r.ld_in + head * 128;
+        float x[2] = {qi[lane], qi[lane + 64]};
+        for (int z = 1; z < r.nin; z++) {
+            x[0] = x[0] + qi[z * zs + lane];
+            x[1] = x[1] + qi[z * zs + lane + 64];
+        }
+        float o[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const float y = __shfl_xor(x[j], 1, 64);
+            const int d = lane + 64 * j, i = d >> 1;
+            const float x0 = (d & 1) ? y : x[j], x1 = (d & 1) ? x[j] : y;
+            float v = x[j];
+            if (i < r.half) {
+                const float cc = cs[i], sv = sn[i];
+                const float m0 = x0 * cc, m1 = x1 * sv, m2 = x0 * sv, m3 = x1 * cc;
+                v = (d & 1) ? m2 + m3 : m0 - m1;
+            }
+            if (qscaled) v = v * qscale;
+            o[j] = v;
+        }
+        o0 = o[0];
+        o1 = o[1];
+    };
     float q0, q1;
-    {
+    if (a.rope_fused) {
+        rope_q(kvh * a.group + min(wave, a.group - 1), q0, q1);
+    } else {
         const float *q = a.q + (size_t)t * qdim + (kvh * a.group + min(wave, a.group - 1)) * 128;
         q0 = q[lane];
         q1 = q[lane + 64];
     }
+    // the token's own key (logical limit - 1) is in the last chunk: that
+    // workgroup forms it from the partials and stores it to the cache
+    const bool own_chunk = a.rope_fused && c == nchunks - 1;
     {
         float4 kv[kDecLoads], vv[kDecLoads];
 #pragma unroll
@@ -423,7 +481,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
             const int e = tid + 256 * i;
             const int key = e >> 5, d4 = e & 31;
             const bool ok = key < nk;
-            const float4 k4 = kv[i], v4 = vv[i];
+            float4 k4 = kv[i], v4 = vv[i];
+            if (own_chunk && key == nk - 1) {
+                // the new key and value: partials summed, k rotated, stored
+                const size_t off = (size_t)t * r.ld_in + kvh * 128 + 4 * d4;
+                float4 kx = *(const float4 *)(r.k_in + off), vx = *(const float4 *)(r.v_in + off);
+                for (int z = 1; z < r.nin; z++) {
+                    const float4 ku = *(const float4 *)(r.k_in + z * zs + off), vu = *(const float4 *)(r.v_in + z * zs + off);
+                    kx = make_float4(kx.x + ku.x, kx.y + ku.y, kx.z + ku.z, kx.w + ku.w);
+                    vx = make_float4(vx.x + vu.x, vx.y + vu.y, vx.z + vu.z, vx.w + vu.w);
+                }
+                float kr[4] = {kx.x, kx.y, kx.z, kx.w};
+#pragma unroll
+                for (int pp = 0; pp < 2; pp++) {
+                    const int ip = 2 * d4 + pp;
+                    if (ip < r.half) {
+                        const float x0 = kr[2 * pp], x1 = kr[2 * pp + 1], cc = cs[ip], sv = sn[ip];
+                        const float m0 = x0 * cc, m1 = x1 * sv, m2 = x0 * sv, m3 = x1 * cc;
+                        kr[2 * pp] = m0 - m1;
+                        kr[2 * pp + 1] = m2 + m3;
+                    }
+                }
+                k4 = make_float4(kr[0], kr[1], kr[2], kr[3]);
+                v4 = vx;
+                const size_t row = (size_t)kvh * r.cap + slot;
+                *(float4 *)(r.kc + row * 128 + 4 * d4) = k4;
+                *(float4 *)(r.vc + row * 128 + 4 * d4) = v4;
+                uint32_t kh0, kl0, kh1, kl1, vh0, vl0, vh1, vl1;
+                split2_rtz(k4.x, k4.y, kh0, kl0);
+                split2_rtz(k4.z, k4.w, kh1, kl1);
+                split2_rtz(v4.x, v4.y, vh0, vl0);
+                split2_rtz(v4.z, v4.w, vh1, vl1);
+                *(uint2 *)(r.kp + (row * 2 + 0) * 128 + 4 * d4) = make_uint2(kh0, kh1);
+                *(uint2 *)(r.kp + (row * 2 + 1) * 128 + 4 * d4) = make_uint2(kl0, kl1);
+                *(uint2 *)(r.vp + (row * 2 + 0) * 128 + 4 * d4) = make_uint2(vh0, vh1);
+                *(uint2 *)(r.vp + (row * 2 + 1) * 128 + 4 * d4) = make_uint2(vl0, vl1);
+            }
             *(float4 *)(Ks + key * kDecRow + 4 * d4) =
                 make_float4(ok ? k4.x : 0.f, ok ? k4.y : 0.f, ok ? k4.z : 0.f, ok ? k4.w : 0.f);
             *(float4 *)(Vs + key * 128 + 4 * d4) =
@@ -437,9 +530,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         const int head = kvh * a.group + min(h, a.group - 1);
         __syncthreads(); // K/V staged; the previous head's qs/ps consumed
         if (h0 > 0) {
-            const float *q = a.q + (size_t)t * qdim + head * 128;
-            q0 = q[lane];
-            q1 = q[lane + 64];
+            if (a.rope_fused) {
+                rope_q(head, q0, q1);
+            } else {
+                const float *q = a.q + (size_t)t * qdim + head * 128;
+                q0 = q[lane];
+                q1 = q[lane + 64];
+            }
         }
         qs[wave][lane] = q0;
         qs[wave][lane + 64] = q1;
@@ -539,6 +636,10 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
     if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
+    if (a.rope_fused && (a.T != 1 || a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
+                         !a.rope.k_in || !a.rope.v_in || !a.rope.kc || !a.rope.vc || !a.rope.kp || !a.rope.vp ||
+                         !a.rope.freqs || a.rope.kc != a.kc || a.rope.vc != a.vc))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

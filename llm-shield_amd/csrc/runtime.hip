@@ -635,7 +635,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.mscale = c->mscale;
         ra.orig_ctx = f.rope_original_context;
         ra.temp_scale = f.attention_temperature_scale;
-        HIP_TRY(launch_rope_store(ra, s));
+        // one token: RoPE and the KV store run inside the decode attention kernel
+        if (T != 1) HIP_TRY(launch_rope_store(ra, s));
 
         if (T == 1) {
             DecodeAttnArgs da;
@@ -657,6 +658,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.scale = scale;
             da.part = c->part.p;
             da.ctx = c->ctx32.p;
+            da.rope_fused = 1;
+            da.rope = ra;
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                          8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
             HIP_TRY(launch_attn_decode(da, s));
