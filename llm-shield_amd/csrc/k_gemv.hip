@@ -122,7 +122,9 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int NW = SWIGLU ? 2 : 1; // weights per row (gate and up)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave-uniform in a scalar register: the loads' scalar offsets depend on
+    // it, and a vector value would wrap each load in a one-pass loop
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, rl = lane & 15;
     const int nb = a.K >> 5;
     const int z = blockIdx.y;
