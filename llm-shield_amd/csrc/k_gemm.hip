@@ -180,7 +180,9 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     const int tile_n = (Lp % group) / gsz;
     if (tile_m >= mt || tile_n >= nt) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave-uniform in a scalar register (a vector value can turn the loads'
+    // scalar offsets into per-lane loops)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int M = a.M, K = a.K, nblk = K >> 5;
     // this split's K blocks: [kb_begin, kb_begin + nb)

@@ -170,6 +170,21 @@ def test_other_block_types(gpu, t):
     m.close()
 
 
+@pytest.mark.parametrize("t", [jev.TYPE_Q8_0, jev.TYPE_Q4_0, jev.TYPE_Q5_1])
+@pytest.mark.parametrize("n", [70, 600])
+def test_projection_segments_off_the_wide_tile_grid(gpu, t, n):
+    # 3 query heads over 1 KV head: the fused QKV segments (384, 128, 128 rows)
+    # do not split on 256-row boundaries, so the projections take the
+    # dequant-in-LDS GEMM (small and large batch shapes) instead of B-direct.
+    cfg = tiny_config(n_heads=3, n_kv_heads=1, initial_kv_capacity=1024)
+    synth = jev.SynthModel(cfg, t)
+    m = synth.open(0)
+    r = oracle.OracleModel(cfg).bind_synth(synth)
+    tokens = jev.random_tokens(n, 2048, n + t)
+    assert worst_close(r.forward(tokens), m.forward(tokens)) <= 1e-3
+    m.close()
+
+
 # ---------------------------------------------------------------- error paths
 
 def test_errors_match_reference_exceptions(model):
