@@ -6,6 +6,8 @@ from .model import MINISTRAL_3B, MinistralModel, ModelConfig, TokenLayout, margi
 from .gguf import GgufFile, GgufTensorInfo, NotSupportedError, bind_gguf, config_from_gguf, load_gguf, write_gguf
 from .synth import SEED, VERDICT_NO, VERDICT_YES, SynthModel, quantize, random_tokens, synth_tensor
 from .weight import QuantWeight, get_matmul_strategy, quantize_activations, set_matmul_strategy
+from .prefix_cache import InvalidOperationError, SystemPromptCache
+from .decider import DecisionResult, TreeDecider, common_prefix, temperature_for
 
 __all__ = [
     "ArgumentError", "CancelledError", "DataError", "GgufFile", "GgufTensorInfo", "JevError", "NotSupportedError",
@@ -14,4 +16,5 @@ __all__ = [
     "TYPE_NAMES", "TYPE_Q4_0", "TYPE_Q5_1", "TYPE_Q8_0", "TokenLayout", "VERDICT_NO", "VERDICT_YES", "lib",
     "margins", "quantize", "random_tokens", "row_bytes", "synth_tensor", "MATMUL_AUTO", "MATMUL_FLOAT",
     "MATMUL_INTEGER", "get_matmul_strategy", "quantize_activations", "set_matmul_strategy",
+    "InvalidOperationError", "SystemPromptCache", "DecisionResult", "TreeDecider", "common_prefix", "temperature_for",
 ]

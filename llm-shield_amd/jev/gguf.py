@@ -319,6 +319,7 @@ def config_from_gguf(g: GgufFile, initial_kv_capacity: int = 512) -> ModelConfig
         rope_attn_factor=f2(a + "rope.scaling.attn_factor", a + "rope.scaling.yarn_attn_factor", 1.0),
         attention_temperature_scale=f2(a + "attention.temperature_scale", a + "rope.scaling_beta", 0.0),
         initial_kv_capacity=initial_kv_capacity,
+        architecture=arch,
     )
     if cfg.n_kv_heads == 0 or cfg.n_heads % cfg.n_kv_heads != 0:
         raise L.DataError(L.JEV_EDATA, f"{cfg.n_heads} attention heads do not divide into {cfg.n_kv_heads} KV heads.")
@@ -373,6 +374,7 @@ def load_gguf(path: str, device: int = 0, initial_kv_capacity: int = 512) -> Min
         except BaseException:
             model.close()
             raise
+    model.model_path = path
     return model
 
 

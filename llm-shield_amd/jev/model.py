@@ -40,6 +40,9 @@ class ModelConfig:
     rope_attn_factor: float = 1.0
     attention_temperature_scale: float = 0.0
     initial_kv_capacity: int = 512
+    # general.architecture (ModelConfig.cs:14); host-side only, part of a
+    # prefix snapshot's fingerprint
+    architecture: str = "mistral3"
 
     @property
     def qdim(self) -> int:
@@ -52,7 +55,8 @@ class ModelConfig:
     def to_c(self) -> L.Config:
         c = L.Config()
         for f in fields(self):
-            setattr(c, f.name, getattr(self, f.name))
+            if f.name != "architecture":
+                setattr(c, f.name, getattr(self, f.name))
         return c
 
 
@@ -142,6 +146,9 @@ class MinistralModel:
 
     def __init__(self, config: ModelConfig, device: int = 0):
         self.config = config
+        # MinistralModel.ModelPath (MinistralModel.cs:51): the GGUF file the
+        # weights came from, None for weights bound from memory
+        self.model_path: Optional[str] = None
         self._lib = L.lib()
         h = ctypes.c_void_p()
         L.check(self._lib.jev_create(ctypes.byref(config.to_c()), device, ctypes.byref(h)))
