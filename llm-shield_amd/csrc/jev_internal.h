@@ -141,6 +141,18 @@ inline int gemm_choose_split(int N, int K)
 // y[m][n] = sum_z partial[z][m][n] (+ res[m][n] if res), z ascending.
 hipError_t launch_reduce_partials(const float *partial, int ksplit, int M, int N, float *y, hipStream_t s);
 
+// One token's decode attention before its chunks are combined: per-chunk
+// partials (max, sum, o[128]) of every head, [heads][max_chunks][130], and
+// what fixes the token's visible-key count -- the layout arrays (entry 0) or
+// the causal start (read from start_dev when set).
+struct DecodeChunks {
+    const float *part = nullptr;
+    int max_chunks = 0;
+    const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
+    int start = 0;
+    const int32_t *start_dev = nullptr;
+};
+
 // GEMV for one token: y[r] = dot(x, W[r]) with fp32 x.  Up to 3 segments
 // (outputs concatenated), or a gate/up pair with SwiGLU fused (y = silu(g)*u).
 struct GemvArgs {
@@ -154,6 +166,9 @@ struct GemvArgs {
     // x_up > 0: x holds a gate row and, x_up floats later, an up row; the
     // input is Kernels.SwiGlu of the pair (silu(g) * u), formed while staging
     int x_up = 0;
+    // attn.part set: x is unused; the input is the decode attention output,
+    // its chunks merged in ascending order while staging
+    DecodeChunks attn;
 };
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 // GEMV shape rules, functions of the weight shape only.  Many rows: each wave
@@ -235,7 +250,7 @@ struct AttnArgs {
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 
 // Decode attention: one query token per entry, split over kDecodeKeys-key
-// chunks, partials combined in chunk order.  ctx fp32 [T][qdim].
+// chunks; leaves per-chunk partials for the consumer (GemvArgs::attn).
 constexpr int kDecodeKeys = 64;
 struct DecodeAttnArgs {
     int T = 0, n_heads = 0, group = 4, hd = 128, max_chunks = 0;
@@ -247,7 +262,6 @@ struct DecodeAttnArgs {
     const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     float scale = 0.f;
     float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
-    float *ctx = nullptr;
     // One token (T = 1) with rope_fused: RoPE and the KV store happen here --
     // q from the projection partials of `rope` (q_in / k_in / v_in, nin,
     // in_stride, the frequency and scaling fields), the new key and value

@@ -30,9 +30,9 @@
 //   O^T (128 x 32) += V^T (128 x 64) . P^T (64 x 32)      48 MFMAs per 64 keys,
 //                     keys taken in the order the S^T fragments hold them
 //
-// Decode kernel (attn_decode_kernel): few tokens, one query per head, split
-// over chunks of 64 logical keys per KV head; chunks combined in ascending
-// order by a second, small kernel.
+// Decode kernel (attn_decode_kernel): one query per head, split over chunks
+// of 64 logical keys per KV head; the chunks are combined in ascending order
+// by the consumer, the O projection's GEMV, while it stages its input.
 #include "jev_dev.h"
 
 namespace jev {
@@ -371,8 +371,11 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 // and V rows are staged in LDS once with coalesced loads and serve the
 // group's query heads (wave w takes heads w, w + 4, ...).  Scores: lane =
 // key, fp32 dot over 128 dims; weighted sum: lane = two dims.  Each chunk
-// leaves (max, sum, o[128]) per head; attn_decode_combine_kernel then sums
-// the chunks in ascending order, so the result does not depend on timing.
+// leaves (max, sum, o[128]) per head.  The GEMV of the O projection merges
+// the chunks in ascending order while staging its input (the kernel boundary
+// makes the partials visible; a last-to-finish merge here would need a
+// device-scope fence per workgroup, an L2 write-back and invalidate on this
+// multi-XCD part), so the result does not depend on timing.
 constexpr int kDecKeys = kDecodeKeys;
 constexpr int kDecRow = 132; // padded K row, floats
 constexpr int kDecLoads = kDecKeys * 32 / 256; // float4 loads of K (and of V) per thread
@@ -582,59 +585,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     }
 }
 
-// Chunks of one (token, query head) combined in ascending order.  A kernel of
-// its own: the kernel boundary makes the partials visible, where a
-// last-to-finish combine would need a device-scope fence per workgroup (an L2
-// write-back and invalidate on this multi-XCD part).
-__global__ __launch_bounds__(64) void attn_decode_combine_kernel(DecodeAttnArgs a)
-{
-    const int t = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
-    const int qdim = a.n_heads * 128;
-    const int start = a.start_dev ? *a.start_dev : a.start;
-    const int slot = a.slot ? a.slot[t] : start + t;
-    const int slo = a.shared_lo ? a.shared_lo[t] : 0;
-    const int shi = a.shared_hi ? a.shared_hi[t] : start;
-    const int seg = a.segment ? a.segment[t] : start;
-    const int limit = (shi - slo) + (slot - seg + 1);
-    const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
-    const float *part = a.part + (((size_t)t * a.n_heads) * a.max_chunks + (size_t)head * a.max_chunks) * 130;
-    // eight loads in flight at a time
-    float M = -INFINITY;
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
-        float mv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) mv[j] = part[min(c0 + j, nchunks - 1) * 130];
-#pragma unroll
-        for (int j = 0; j < 8; j++) M = fmaxf(M, mv[j]);
-    }
-    float L = 0.f, O0 = 0.f, O1 = 0.f;
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
-        float mv[8], lv[8];
-        float2 ov[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float *pc = part + min(c0 + j, nchunks - 1) * 130;
-            mv[j] = pc[0];
-            lv[j] = pc[1];
-            ov[j] = *(const float2 *)(pc + 2 + 2 * lane);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (c0 + j < nchunks) {
-                const float f = __expf(mv[j] - M);
-                L = fmaf(lv[j], f, L);
-                O0 = fmaf(ov[j].x, f, O0);
-                O1 = fmaf(ov[j].y, f, O1);
-            }
-        }
-    }
-    float *ctx = a.ctx + (size_t)t * qdim + head * 128;
-    *(float2 *)(ctx + 2 * lane) = make_float2(O0 / L, O1 / L);
-}
-
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
+    if (a.T != 1) return hipErrorInvalidValue; // one token: its consumer reads entry 0
     if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
     if (a.rope_fused && (a.T != 1 || a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
                          !a.rope.k_in || !a.rope.v_in || !a.rope.kc || !a.rope.vc || !a.rope.kp || !a.rope.vp ||
@@ -643,7 +597,6 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
     hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_decode_combine_kernel, dim3(a.T, a.n_heads), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

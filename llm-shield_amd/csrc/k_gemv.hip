@@ -117,7 +117,8 @@ struct TileLoader {
 // WR, ksplit).  nbz: quant blocks per K split (even).  DEPTH: tiles (block
 // pairs) per pipeline stage, chosen per shape so that a wave's last stage
 // carries few clamped reloads.
-template <int TYPE, int WR, bool SWIGLU, int DEPTH>
+// ATTN: the input is the decode attention output (GemvArgs::attn).
+template <int TYPE, int WR, bool SWIGLU, int DEPTH, bool ATTN>
 __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -168,11 +169,60 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
     uint16_t *xh = (uint16_t *)smem, *xl = xh + nbz * 32, *zero = xl + nbz * 32;
     float *xsum = (float *)(zero + 8);
     float *red = xsum + nbz; // [4][NW][16] wave partials
+    // decode attention input: the token's chunk count, as the attention
+    // kernel computes it
+    int nch = 0;
+    if (ATTN) {
+        const DecodeChunks &d = a.attn;
+        const int start = d.start_dev ? *d.start_dev : d.start;
+        const int slot = d.slot ? d.slot[0] : start;
+        const int slo = d.shared_lo ? d.shared_lo[0] : 0;
+        const int shi = d.shared_hi ? d.shared_hi[0] : start;
+        const int seg = d.segment ? d.segment[0] : start;
+        const int limit = (shi - slo) + (slot - seg + 1);
+        nch = min((limit + kDecodeKeys - 1) / kDecodeKeys, d.max_chunks);
+    }
     // thread -> 8 consecutive elements; a block's four groups are neighbouring lanes
     for (int i0 = 0; i0 < 2 * ntw * 4; i0 += 256) {
         const int i = i0 + tid;
         float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (i < nbw * 4) {
+        if (ATTN && i < nbw * 4) {
+            // the decode attention output for these 8 dims of one head: the
+            // chunks' (max, sum, o) merged in ascending chunk order with a
+            // running max (each step rescales what came before by
+            // exp(old max - new max)), eight chunks' loads in flight at a time
+            const int k = kb0 * 32 + 8 * i, d = k & 127;
+            const float *pp = a.attn.part + (size_t)(k >> 7) * a.attn.max_chunks * 130;
+            float M = -INFINITY, L = 0.f;
+            for (int c0 = 0; c0 < nch; c0 += 8) {
+                float mv[8], lv[8];
+                float2 ov[8][4];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float *pc = pp + min(c0 + j, nch - 1) * 130; // clamped reloads are unused
+                    mv[j] = pc[0];
+                    lv[j] = pc[1];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) ov[j][e] = *(const float2 *)(pc + 2 + d + 2 * e);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (c0 + j < nch) {
+                        const float Mn = fmaxf(M, mv[j]);
+                        const float fo = __expf(M - Mn), fc = __expf(mv[j] - Mn);
+                        L = fmaf(lv[j], fc, L * fo);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            v[2 * e] = fmaf(ov[j][e].x, fc, v[2 * e] * fo);
+                            v[2 * e + 1] = fmaf(ov[j][e].y, fc, v[2 * e + 1] * fo);
+                        }
+                        M = Mn;
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = v[e] / L;
+        } else if (i < nbw * 4) {
             const float4 *xp = (const float4 *)(a.x + (size_t)kb0 * 32 + 8 * i);
             const float4 v0 = xp[0], v1 = xp[1];
             v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
@@ -288,7 +338,7 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
     }
 }
 
-template <int TYPE, int WR, bool SWIGLU>
+template <int TYPE, int WR, bool SWIGLU, bool ATTN = false>
 static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
 {
     const int nb = a.K >> 5;
@@ -301,9 +351,9 @@ static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
     const int ntw = nbz / 2, per = WR == 4 ? ntw : (ntw + 3) / 4;
     const int pad4 = (per + 3) / 4 * 4 - per, pad2 = (per + 1) / 2 * 2 - per;
     if (pad2 < pad4)
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 2>), grid, dim3(256), lds, s, a, rows, nbz);
+        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 2, ATTN>), grid, dim3(256), lds, s, a, rows, nbz);
     else
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 4>), grid, dim3(256), lds, s, a, rows, nbz);
+        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 4, ATTN>), grid, dim3(256), lds, s, a, rows, nbz);
     return hipGetLastError();
 }
 
@@ -313,6 +363,10 @@ static hipError_t launch_gemv_typed(const GemvArgs &a, hipStream_t s)
     if (a.swiglu) return launch_gemv_cfg<TYPE, 1, true>(a, a.seg[0].rows, s);
     int rows = 0;
     for (int i = 0; i < a.nseg; i++) rows += a.seg[i].rows;
+    if (a.attn.part) {
+        if (gemv_rows_mode(rows)) return launch_gemv_cfg<TYPE, 4, false, true>(a, rows, s);
+        return launch_gemv_cfg<TYPE, 1, false, true>(a, rows, s);
+    }
     if (gemv_rows_mode(rows)) return launch_gemv_cfg<TYPE, 4, false>(a, rows, s);
     return launch_gemv_cfg<TYPE, 1, false>(a, rows, s);
 }
@@ -320,6 +374,9 @@ static hipError_t launch_gemv_typed(const GemvArgs &a, hipStream_t s)
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s)
 {
     if (a.K % 32 != 0 || a.K <= 0 || a.ksplit < 1 || a.x_up < 0 || a.x_up % 4 != 0) return hipErrorInvalidValue;
+    // the attention input: 128-dim heads, one weight, no other input transform
+    if (a.attn.part && (a.K % 128 != 0 || a.x_up || a.swiglu || a.nseg != 1 || a.attn.max_chunks < 1))
+        return hipErrorInvalidValue;
     const int nb = a.K >> 5;
     if (a.ksplit > 1 && (a.swiglu || gemm_split_blocks(nb, a.ksplit) * (a.ksplit - 1) >= nb)) return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; i++) {

@@ -115,7 +115,7 @@ struct jev_ctx {
     int cap = 0, len = 0;
 
     // workspace
-    DevBuf<float> h, y, yo, ydown, q, x32, ctx32, f32, xn, logits, part, xsum;
+    DevBuf<float> h, y, yo, ydown, q, x32, f32, xn, logits, part, xsum;
     DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
     DevBuf<int32_t> ints;
     DevBuf<AttnTile> tiles;
@@ -334,8 +334,10 @@ bool same_type3(const QWeight &a, const QWeight &b, const QWeight &c) { return a
 // `ksplit` K-split partials T * ldy floats apart.  T >= 2: MFMA GEMM on the
 // fp16 pair in the operand-tile layout; T == 1: GEMV on fp32 x.
 // x_up (one token): x32 holds gate | up rows and the GEMV's input is their SwiGLU.
+// attn (one token): the GEMV's input is the decode attention output, combined
+// from its chunk partials while staging (x32 unused).
 int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *xt, const float *xsum,
-           const float *x32, float *y, int ldy, int ksplit, int x_up = 0)
+           const float *x32, float *y, int ldy, int ksplit, int x_up = 0, const DecodeChunks *attn = nullptr)
 {
     double nrows = 0, wbytes = 0;
     for (int i = 0; i < nw; i++) {
@@ -352,6 +354,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
         g.y = y;
         g.ksplit = ksplit;
         g.x_up = x_up;
+        if (attn) g.attn = *attn;
         ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows));
         HIP_TRY(launch_gemv(g, c->stream));
         return JEV_OK;
@@ -384,7 +387,6 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
     HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + 1));
     if (T == 1) {
         HIP_TRY(c->x32.ensure((size_t)std::max<size_t>(f.hidden, 1)));
-        HIP_TRY(c->ctx32.ensure((size_t)c->qdim()));
         HIP_TRY(c->f32.ensure((size_t)2 * f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
     } else {
@@ -637,6 +639,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.temp_scale = f.attention_temperature_scale;
         // one token: RoPE and the KV store run inside the decode attention kernel
         if (T != 1) HIP_TRY(launch_rope_store(ra, s));
+        DecodeChunks dchunks;
 
         if (T == 1) {
             DecodeAttnArgs da;
@@ -657,9 +660,17 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.start_dev = dpos;
             da.scale = scale;
             da.part = c->part.p;
-            da.ctx = c->ctx32.p;
             da.rope_fused = 1;
             da.rope = ra;
+            // the O GEMV merges the chunks while staging its input
+            dchunks.part = da.part;
+            dchunks.max_chunks = da.max_chunks;
+            dchunks.slot = da.slot;
+            dchunks.shared_lo = da.shared_lo;
+            dchunks.shared_hi = da.shared_hi;
+            dchunks.segment = da.segment;
+            dchunks.start = da.start;
+            dchunks.start_dev = da.start_dev;
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                          8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
             HIP_TRY(launch_attn_decode(da, s));
@@ -685,7 +696,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         }
         {
             const QWeight *wo[1] = {&L.o};
-            int rc = linear(c, T, wo, 1, c->xt.p, c->xsum.p, c->ctx32.p, c->yo.p, D, s_o);
+            int rc = linear(c, T, wo, 1, c->xt.p, c->xsum.p, nullptr, c->yo.p, D, s_o, 0,
+                            T == 1 ? &dchunks : nullptr);
             if (rc) return rc;
         }
 
@@ -931,7 +943,7 @@ void jev_destroy(jev_ctx *c)
     if (c->kp) (void)hipFree(c->kp);
     if (c->vp) (void)hipFree(c->vp);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
-    c->x32.release(); c->ctx32.release(); c->f32.release(); c->xn.release(); c->logits.release();
+    c->x32.release(); c->f32.release(); c->xn.release(); c->logits.release();
     c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);

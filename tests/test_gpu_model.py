@@ -62,6 +62,22 @@ def test_prefill_then_decode_steps(model, ref):
     assert model.cached_token_count == 50
 
 
+@pytest.mark.parametrize("ctx", [30, 600])
+def test_single_token_passes_match_oracle(model, ref, ctx):
+    # One-token passes: the O projection forms the attention output from the
+    # decode attention's 64-key chunks while staging its input (600 keys: 10
+    # chunks, more than one group of eight loads in flight).
+    tokens = jev.random_tokens(ctx + 3, 2048, 70 + ctx)
+    fresh(model).prefill(tokens[:ctx])
+    fresh(ref).prefill(tokens[:ctx])
+    for t in tokens[ctx:]:
+        assert worst_close(ref.forward([t]), model.forward([t])) <= 1e-3
+    # a one-token branch after the prefix: the same path under a tree layout
+    g = model.forward_branches([[int(tokens[1])]], ROWS)
+    e = ref.forward_branches([[int(tokens[1])]], ROWS)
+    assert worst_close(np.array(e), np.array(g)) <= 1e-3
+
+
 def test_tree_verdicts_match_oracle(model, ref):
     trunk = jev.random_tokens(100, 2048, 5)
     branches = [jev.random_tokens(n, 2048, 50 + n) for n in (48, 17, 1, 64, 70)]
