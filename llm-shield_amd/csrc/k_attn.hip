@@ -78,8 +78,14 @@ __device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
 }
 } // namespace
 
+// DS = 2 (grids smaller than the GPU): two workgroups per tile and KV head
+// (blockIdx.z); both stage the blocks and compute the scores and softmax (the
+// same instructions on the same data), and each accumulates half of the
+// output dims.  Every output is the same chain of MFMAs either way.
+template <int DS>
 __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 {
+    constexpr int ND = 4 / DS; // 32-dim output tiles per wave
     // Double-buffered K and V blocks as fp16 pairs: [key][hi, lo][16 chunks of
     // 8 dims], chunks swizzled per key (chunk ^ swz(key)) so that both the
     // K fragment reads and the V transpose reads hit distinct banks.
@@ -91,6 +97,7 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     const int hsets = (a.group + 3) >> 2;
     const int kvh = blockIdx.x / hsets;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int dh = DS == 2 ? (int)blockIdx.z : 0; // output dims 64 dh .. (DS = 2)
     const int g = lane >> 5, col = lane & 31;
     const int hl = (blockIdx.x % hsets) * 4 + wave; // query head within the group
     const bool head_ok = hl < a.group;              // wave-uniform
@@ -189,9 +196,9 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
             }
     }
 
-    floatx16 o[4];
+    floatx16 o[ND]; // output dims 32 (ND dh + d) ..
 #pragma unroll
-    for (int d = 0; d < 4; d++)
+    for (int d = 0; d < ND; d++)
 #pragma unroll
         for (int j = 0; j < 16; j++) o[d][j] = 0.f;
     float m_run = -INFINITY, l_run = 0.f; // running max in log2 units
@@ -250,12 +257,13 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
         // slot 8 g + i is key 16 c + 8 (i / 4) + 4 g + i % 4: the P values
         // sc[c / 2][8 (c % 2) + i] of this lane, split into pbh / pbl.
         if (b >= 1) {
-            // 16 steps (chunk c, dim tile d); the V^T fragments of the step
-            // after next are read while this step's three MFMAs run
+            // 4 ND steps (chunk c, dim tile d); the V^T fragments of the
+            // step after next are read while this step's three MFMAs run
+            constexpr int NST = 4 * ND;
             const char *vb = (const char *)Vp;
             uint2 vf[3][4];
             auto vread = [&](int st, uint2 (&f)[4]) __attribute__((always_inline)) {
-                const int c = st >> 2, d = st & 3;
+                const int c = st / ND, d = ND * dh + st % ND;
                 const char *v0 = vb + c * (16 * 512) + voff[0][d];
                 const char *v1 = vb + c * (16 * 512) + voff[1][d];
                 f[0] = read_tr(v0);
@@ -266,9 +274,9 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
             vread(0, vf[0]);
             vread(1, vf[1]);
 #pragma unroll
-            for (int st = 0; st < 16; st++) {
-                const int c = st >> 2, d = st & 3;
-                if (st + 2 < 16) vread(st + 2, vf[(st + 2) % 3]);
+            for (int st = 0; st < NST; st++) {
+                const int c = st / ND, d = st % ND;
+                if (st + 2 < NST) vread(st + 2, vf[(st + 2) % 3]);
                 const uint2(&f)[4] = vf[st % 3];
                 const half8_t vh = cat4(f[0], f[1]), vl = cat4(f[2], f[3]);
                 o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
@@ -277,8 +285,8 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
             }
             __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
 #pragma unroll
-            for (int st = 0; st < 16; st++) {
-                if (st + 2 < 16) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+            for (int st = 0; st < NST; st++) {
+                if (st + 2 < NST) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
                 __builtin_amdgcn_sched_group_barrier(0x008, 3, 1);
             }
         }
@@ -327,7 +335,7 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
         // block b - 1's P V, before block b's)
         if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-            for (int d = 0; d < 4; d++)
+            for (int d = 0; d < ND; d++)
 #pragma unroll
                 for (int j = 0; j < 16; j++) o[d][j] = o[d][j] * alpha;
         }
@@ -338,15 +346,15 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     }
 
     if (q_ok) {
-        // o[d][j] is dim 32 d + 8 (j / 4) + 4 g + j % 4: four consecutive k, one
-        // 8-byte store per part
+        // o[d][j] is dim 32 (ND dh + d) + 8 (j / 4) + 4 g + j % 4: four
+        // consecutive k, one 8-byte store per part
         const float inv = 1.0f / l_run;
         const int t = tile.t0 + col, nblk = qdim >> 5;
 #pragma unroll
-        for (int d = 0; d < 4; d++)
+        for (int d = 0; d < ND; d++)
 #pragma unroll
             for (int jq = 0; jq < 4; jq++) {
-                const int k = head * 128 + 32 * d + 8 * jq + 4 * g;
+                const int k = head * 128 + 32 * (ND * dh + d) + 8 * jq + 4 * g;
                 uint2 hv, lv;
                 split4(make_float4(o[d][4 * jq] * inv, o[d][4 * jq + 1] * inv, o[d][4 * jq + 2] * inv,
                                    o[d][4 * jq + 3] * inv), hv, lv);
@@ -361,7 +369,12 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
     if (a.n_tiles <= 0) return hipSuccess;
     if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp) return hipErrorInvalidValue;
     const int n_kv = a.n_heads / a.group, hsets = (a.group + 3) / 4;
-    hipLaunchKernelGGL(attn_tree_kernel, dim3(n_kv * hsets, a.n_tiles), dim3(256), 0, s, a);
+    const dim3 grid(n_kv * hsets, a.n_tiles);
+    // fewer workgroups than compute units: the output dims split over two
+    if ((long)grid.x * grid.y < 256)
+        hipLaunchKernelGGL(attn_tree_kernel<2>, dim3(grid.x, grid.y, 2), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attn_tree_kernel<1>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -108,6 +108,24 @@ def test_tree_equals_branches_alone_bitwise(model):
         assert np.array_equal(alone[b], cached[b]), b
 
 
+def test_tree_equals_branches_alone_across_attention_grids(model):
+    # A 4100-token trunk: the tree pass's attention grid (one workgroup per
+    # 32-token tile and KV head) covers the GPU, so each workgroup computes all
+    # 128 output dims; the short branches alone split the dims over two
+    # workgroups.  The bits must not change.
+    prefix = jev.random_tokens(4100, 2048, 21)
+    branches = [jev.random_tokens(n, 2048, 90 + n) for n in (40, 3)]
+    m = fresh(model)
+    m.prefill(prefix)
+    alone = []
+    for b in branches:
+        m.kv_truncate(len(prefix))
+        alone.append(m.forward_selected(b, ROWS))
+    tree = fresh(m).forward_tree(prefix, branches, ROWS)
+    for b in range(len(branches)):
+        assert np.array_equal(alone[b], tree[b]), b
+
+
 def test_cached_prefix_equals_whole_prompt_bitwise(model):
     tokens = jev.random_tokens(120, 2048, 9)
     m = fresh(model)
