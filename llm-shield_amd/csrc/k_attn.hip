@@ -78,10 +78,10 @@ __device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
 }
 } // namespace
 
-// DS = 2 (grids smaller than the GPU): two workgroups per tile and KV head
-// (blockIdx.z); both stage the blocks and compute the scores and softmax (the
-// same instructions on the same data), and each accumulates half of the
-// output dims.  Every output is the same chain of MFMAs either way.
+// DS = 2 or 4 (grids smaller than the GPU): DS workgroups per tile and KV
+// head (blockIdx.z); each stages the blocks and computes the scores and
+// softmax (the same instructions on the same data) and accumulates 128 / DS
+// of the output dims.  Every output is the same chain of MFMAs either way.
 template <int DS>
 __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 {
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     const int hsets = (a.group + 3) >> 2;
     const int kvh = blockIdx.x / hsets;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int dh = DS == 2 ? (int)blockIdx.z : 0; // output dims 64 dh .. (DS = 2)
+    const int dh = DS > 1 ? (int)blockIdx.z : 0; // output dims 128 / DS * dh ..
     const int g = lane >> 5, col = lane & 31;
     const int hl = (blockIdx.x % hsets) * 4 + wave; // query head within the group
     const bool head_ok = hl < a.group;              // wave-uniform
@@ -370,8 +370,11 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
     if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp) return hipErrorInvalidValue;
     const int n_kv = a.n_heads / a.group, hsets = (a.group + 3) / 4;
     const dim3 grid(n_kv * hsets, a.n_tiles);
-    // fewer workgroups than compute units: the output dims split over two
-    if ((long)grid.x * grid.y < 256)
+    // fewer workgroups than compute units: the output dims split over two or four
+    const long wgs = (long)grid.x * grid.y;
+    if (wgs <= 64)
+        hipLaunchKernelGGL(attn_tree_kernel<4>, dim3(grid.x, grid.y, 4), dim3(256), 0, s, a);
+    else if (wgs < 256)
         hipLaunchKernelGGL(attn_tree_kernel<2>, dim3(grid.x, grid.y, 2), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(attn_tree_kernel<1>, grid, dim3(256), 0, s, a);

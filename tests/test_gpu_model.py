@@ -108,12 +108,15 @@ def test_tree_equals_branches_alone_bitwise(model):
         assert np.array_equal(alone[b], cached[b]), b
 
 
-def test_tree_equals_branches_alone_across_attention_grids(model):
-    # A 4100-token trunk: the tree pass's attention grid (one workgroup per
-    # 32-token tile and KV head) covers the GPU, so each workgroup computes all
-    # 128 output dims; the short branches alone split the dims over two
-    # workgroups.  The bits must not change.
-    prefix = jev.random_tokens(4100, 2048, 21)
+@pytest.mark.parametrize("trunk", [2100, 4100])
+def test_tree_equals_branches_alone_across_attention_grids(model, trunk):
+    # The attention grid has one workgroup per 32-token tile and KV head; grids
+    # smaller than the GPU split the 128 output dims over 2 (up to 255
+    # workgroups) or 4 (up to 64) workgroups.  With this model's 2 KV heads a
+    # 4100-token tree pass computes all dims per workgroup, a 2100-token one
+    # splits them in two, the short branches alone in four.  The bits must not
+    # change.
+    prefix = jev.random_tokens(trunk, 2048, 21)
     branches = [jev.random_tokens(n, 2048, 90 + n) for n in (40, 3)]
     m = fresh(model)
     m.prefill(prefix)
