@@ -22,11 +22,50 @@ hipError_t launch_dequant(const QWeight &w, float *dst, hipStream_t s)
 }
 
 // QuantMatMul.GatherRows (QuantMatMul.cs:294-305): ids are validated on the host.
-__global__ void gather_kernel(QWeight w, const int32_t *ids, float *h)
+// A thread decodes 8 consecutive elements -- one lane slot of a tile, so one
+// load of their quants and one of the block scale -- with decode_elem's
+// arithmetic per element.
+__global__ __launch_bounds__(256) void gather_kernel(QWeight w, const int32_t *ids, float *h)
 {
-    int t = blockIdx.x;
-    int r = ids[t];
-    for (int k = threadIdx.x; k < w.cols; k += blockDim.x) h[(size_t)t * w.cols + k] = decode_elem(w, r, k);
+    const int t = blockIdx.x, row = ids[t];
+    const int rg = row >> 4, r = row & 15, kp = tile_kpairs(w.cols), ng = w.cols >> 3;
+    for (int j = threadIdx.x; j < ng; j += 256) {
+        const int k = 8 * j, b = k >> 5, bb = b & 1, l = 16 * ((k & 31) >> 3) + r;
+        const size_t tile = (size_t)rg * kp + (b >> 1);
+        float v[8];
+        if (w.type == kQ8_0) {
+            const float d = h2f(w.d[tile * 32 + 2 * r + bb]);
+            const uint2 q = *(const uint2 *)(w.qs + tile * 1024 + 16 * l + 8 * bb);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int qi = (int)(((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xffu) - 128; // stored biased
+                v[i] = (float)qi * d;
+            }
+        } else {
+            const uint32_t q = *(const uint32_t *)(w.qs + tile * 512 + 8 * l + 4 * bb);
+            if (w.type == kQ4_0) {
+                const float d = h2f(w.d[tile * 32 + 2 * r + bb]);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int nib = (int)((q >> (8 * (i & 3) + (i < 4 ? 0 : 4))) & 15u);
+                    v[i] = d * (float)(nib - 8);
+                }
+            } else {
+                const float d = h2f(w.d[tile * 64 + 4 * r + bb]), m = h2f(w.d[tile * 64 + 4 * r + 2 + bb]);
+                const uint32_t qh = w.qh[tile * 128 + 2 * l + bb];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int nib = (int)((q >> (8 * (i & 3) + (i < 4 ? 0 : 4))) & 15u);
+                    const int qi = nib | (int)(((qh >> i) & 1u) << 4);
+                    const float dq = d * (float)qi;
+                    v[i] = dq + m;
+                }
+            }
+        }
+        float4 *o = (float4 *)(h + (size_t)t * w.cols + k);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
 }
 
 hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, hipStream_t s)
