@@ -173,7 +173,7 @@ void *jev_stream(jev_ctx *ctx);
 #define JEV_PROF_GEMM 0 /* MFMA prefill GEMM                     */
 #define JEV_PROF_ATTN 1 /* tree attention (prefill)              */
 #define JEV_PROF_GEMV 2 /* one-token quantized GEMV              */
-#define JEV_PROF_DECODE_ATTN 3 /* decode attention + combine     */
+#define JEV_PROF_DECODE_ATTN 3 /* decode attention (chunks)      */
 #define JEV_PROF_CLASSES 4
 int jev_profile_enable(jev_ctx *ctx, int enable);
 int jev_profile_read(jev_ctx *ctx, int kernel_class, int64_t *launches, double *total_ms, double *flops,
