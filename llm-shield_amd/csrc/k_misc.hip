@@ -364,8 +364,9 @@ hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
     if (a.n_heads * a.hd > 512 * kRopeIters || a.n_kv * a.hd > 512 * kRopeKv || a.nin < 1 || a.nin > kRopeParts ||
         a.half > 512 || a.hd % 2 != 0 || !a.kp || !a.vp)
         return hipErrorInvalidValue;
-    // few tokens: several workgroups per token share its heads
-    const int split = a.T >= 1024 ? 1 : std::min(8, 1024 / a.T);
+    // few tokens: several workgroups per token share its heads, ~512
+    // workgroups in all (measured at 256 tokens: 2 per token ahead of 1, 4, 8)
+    const int split = a.T >= 512 ? 1 : std::min(8, 512 / a.T);
     hipLaunchKernelGGL(rope_store_kernel, dim3(a.T, split), dim3(256), 0, s, a);
     return hipGetLastError();
 }
