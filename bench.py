@@ -50,36 +50,11 @@ def prof_read(lib, h, cls):
 
 
 def batched_decisions_layout(nd, trunk_n, nb, bl):
-    """Token layout of nd independent trees laid end to end in one KV arena:
-    decision d owns slots [d * per, (d + 1) * per); its trunk is causal from
-    position 0, each branch sees the trunk and itself (positions continue from
-    the trunk), outputs are the branches' last tokens."""
-    import numpy as np
+    """Token layout of nd independent decisions laid end to end in one KV
+    arena, each a trunk of trunk_n tokens and nb branches of bl tokens."""
     import jev
 
-    per = trunk_n + nb * bl
-    total = nd * per
-    slot = np.arange(total, dtype=np.int32)
-    pos = np.empty(total, np.int32)
-    lo = np.empty(total, np.int32)
-    hi = np.empty(total, np.int32)
-    seg = np.empty(total, np.int32)
-    outs = []
-    for d in range(nd):
-        b0 = d * per
-        t = np.arange(trunk_n)
-        pos[b0:b0 + trunk_n] = t
-        lo[b0:b0 + trunk_n] = b0
-        hi[b0:b0 + trunk_n] = b0
-        seg[b0:b0 + trunk_n] = b0
-        for b in range(nb):
-            s0 = b0 + trunk_n + b * bl
-            pos[s0:s0 + bl] = trunk_n + np.arange(bl)
-            lo[s0:s0 + bl] = b0
-            hi[s0:s0 + bl] = b0 + trunk_n
-            seg[s0:s0 + bl] = s0
-            outs.append(s0 + bl - 1)
-    return jev.TokenLayout(slot, pos, hi, seg, np.array(outs, np.int32), total, shared_lo=lo)
+    return jev.TokenLayout.forest([(trunk_n, [bl] * nb)] * nd)
 
 
 def main():

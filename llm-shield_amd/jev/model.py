@@ -121,6 +121,39 @@ class TokenLayout:
             outputs.append(len(slot) - 1)
         return TokenLayout(slot, pos, sh, seg, outputs, end)
 
+    @staticmethod
+    def forest(trees: Sequence[tuple]) -> "TokenLayout":
+        """Independent trees laid end to end in one cache, each (trunk length,
+        [branch lengths]) as TokenLayout.Tree with its own first slot: tree d
+        owns slots [b_d, b_d + its tokens); its trunk is causal from position
+        0, a branch sees its tree's trunk (shared_lo .. shared_hi) and itself
+        (positions continue after the trunk); the outputs are the branches'
+        last tokens, in tree order.  The reference's layouts are the case of
+        one tree (shared_lo = 0): this is the batch of independent decisions."""
+        slot, pos, lo, hi, seg, outputs = [], [], [], [], [], []
+        b0 = 0
+        for trunk, branch_lengths in trees:
+            for t in range(trunk):
+                slot.append(b0 + t)
+                pos.append(t)
+                lo.append(b0)
+                hi.append(b0)
+                seg.append(b0)
+            s0 = b0 + trunk
+            for bl in branch_lengths:
+                if bl <= 0:
+                    raise L.ArgumentError(L.JEV_EINVAL, "Branch is empty.")
+                for i in range(bl):
+                    slot.append(s0 + i)
+                    pos.append(trunk + i)
+                    lo.append(b0)
+                    hi.append(b0 + trunk)
+                    seg.append(s0)
+                outputs.append(len(slot) - 1)
+                s0 += bl
+            b0 = s0
+        return TokenLayout(slot, pos, hi, seg, outputs, b0, shared_lo=lo)
+
     def with_outputs(self, outputs) -> "TokenLayout":
         return TokenLayout(self.slot, self.position, self.shared_hi, self.segment, outputs, self.end, self.shared_lo)
 

@@ -8,7 +8,11 @@ ggml quantizer) -- the model every benchmark row runs.
   branch run alone after the trunk and the branches off a cached trunk
   (DeciderTests.cs:55-91, with the benchmark tree's 9 x 48-token branches),
   and a restored prefix snapshot equals the whole prompt
-  (SystemPromptCacheTests.cs:42-68).
+  (SystemPromptCacheTests.cs:42-68);
+* the batched-decisions layout (independent trees, Q4_0) equals each tree
+  run alone, bit for bit;
+* Q5_1 greedy decode (one step replayed as a HIP graph): every chosen token
+  is the oracle's argmax, teacher-forced, up to the logits bar.
 """
 import os
 
@@ -80,3 +84,40 @@ def test_full_shape_restored_prefix_equals_whole_prompt_bitwise(model):
     model.reset_kv_cache()
     model.kv_restore(snap, 170)
     assert np.array_equal(model.forward(tokens[170:]), whole)
+
+
+def test_full_shape_q4_0_forest_equals_each_tree_alone_bitwise(gpu):
+    synth = jev.SynthModel(jev.ModelConfig(initial_kv_capacity=512), jev.TYPE_Q4_0)
+    trees = [(64, [16, 16, 16]), (40, [8, 24])]
+    with synth.open(0) as m:
+        tokens, alone = [], []
+        for i, (trunk_n, bls) in enumerate(trees):
+            trunk = list(jev.random_tokens(trunk_n, VOCAB, 500 + i))
+            branches = [list(jev.random_tokens(n, VOCAB, 600 + 10 * i + j)) for j, n in enumerate(bls)]
+            tokens += trunk + [t for b in branches for t in b]
+            m.reset_kv_cache()
+            alone += m.forward_tree(trunk, branches, ROWS)
+        lay = jev.TokenLayout.forest(trees)
+        m.reset_kv_cache()
+        got = m.forward_layout(tokens, lay, jev.OUT_SELECTED, ROWS).reshape(len(lay.outputs), len(ROWS))
+    for k in range(len(alone)):
+        assert np.array_equal(got[k], alone[k]), k
+
+
+def test_full_shape_q5_1_greedy_decode_follows_oracle(gpu):
+    synth = jev.SynthModel(jev.ModelConfig(initial_kv_capacity=256), jev.TYPE_Q5_1)
+    prompt = jev.random_tokens(32, VOCAB, 9)
+    with synth.open(0) as m:
+        m.prefill(prompt)
+        out = m.decode_greedy(int(prompt[-1]), 4)
+    oracle.set_threads(max(1, min(16, os.cpu_count() or 1)))
+    ref = oracle.OracleModel(synth.config).bind_synth(synth)
+    try:
+        ref.prefill(prompt)
+        nxt = int(prompt[-1])
+        for tok in out:
+            e = ref.forward([nxt])
+            assert e[tok] >= e.max() - 1e-3 * max(1.0, abs(float(e.max())))
+            nxt = int(tok)
+    finally:
+        ref.close()

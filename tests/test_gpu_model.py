@@ -129,6 +129,22 @@ def test_tree_equals_branches_alone_across_attention_grids(model, trunk):
         assert np.array_equal(alone[b], tree[b]), b
 
 
+def test_forest_equals_each_tree_alone_bitwise(model):
+    # Independent decisions in one pass (TokenLayout.forest: each tree its own
+    # shared range): every branch's verdict rows equal that tree run alone.
+    trees = [(40, [5, 9]), (17, [3]), (64, [1, 20, 7])]
+    tokens, alone = [], []
+    for i, (trunk_n, bls) in enumerate(trees):
+        trunk = list(jev.random_tokens(trunk_n, 2048, 300 + i))
+        branches = [list(jev.random_tokens(n, 2048, 400 + 10 * i + j)) for j, n in enumerate(bls)]
+        tokens += trunk + [t for b in branches for t in b]
+        alone += fresh(model).forward_tree(trunk, branches, ROWS)
+    lay = jev.TokenLayout.forest(trees)
+    got = fresh(model).forward_layout(tokens, lay, jev.OUT_SELECTED, ROWS).reshape(len(lay.outputs), len(ROWS))
+    for k in range(len(alone)):
+        assert np.array_equal(got[k], alone[k]), k
+
+
 def test_cached_prefix_equals_whole_prompt_bitwise(model):
     tokens = jev.random_tokens(120, 2048, 9)
     m = fresh(model)
