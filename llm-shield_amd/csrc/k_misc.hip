@@ -88,8 +88,12 @@ hipError_t launch_gather(const QWeight &w, const int32_t *ids, int n, float *h, 
 constexpr int kNormIters = 8;   // float4 groups per thread: D <= 8192
 constexpr int kNormParts = 4;   // K-split partials
 
+// NI: float4 groups per thread for this D (the registers of the loads in
+// flight are sized for it; 3 for D = 3072).
+template <int NI>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
 {
+    constexpr int kNormIters = NI;
     __shared__ float wsum[4];
     const int t = blockIdx.x, tid = threadIdx.x;
     const int row = a.rows ? a.rows[t] : t;
@@ -193,7 +197,13 @@ hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
     if (a.T <= 0) return hipSuccess;
     if (a.D % 32 != 0 || a.D > 4 * 256 * kNormIters || a.nadd < 1 || a.nadd > kNormParts) return hipErrorInvalidValue;
     if (a.xsum && !a.ot) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.T), dim3(256), 0, s, a);
+    switch ((a.D / 4 + 255) / 256) {
+    case 1: hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(a.T), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(a.T), dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(rmsnorm_kernel<3>, dim3(a.T), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(rmsnorm_kernel<4>, dim3(a.T), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(rmsnorm_kernel<kNormIters>, dim3(a.T), dim3(256), 0, s, a); break;
+    }
     return hipGetLastError();
 }
 
