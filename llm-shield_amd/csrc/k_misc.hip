@@ -90,12 +90,24 @@ constexpr int kNormParts = 4;   // K-split partials
 
 // NI: float4 groups per thread for this D (the registers of the loads in
 // flight are sized for it; 3 for D = 3072).
+// Row of workgroup L: workgroups go to the eight XCDs round robin (L % 8),
+// and the 16 rows of an operand tile share its cache lines, so within each
+// full 128 rows the 16 rows of a tile are given to workgroups of one XCD
+// (its L2 then holds whole lines); rows past the last full 128 map to
+// themselves.
+__device__ __forceinline__ int norm_row(int L, int T)
+{
+    if (L >= (T & ~127)) return L;
+    const int x = L & 7, j = L >> 3;
+    return (j & 15) + 16 * ((j >> 4) * 8 + x);
+}
+
 template <int NI>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
 {
     constexpr int kNormIters = NI;
     __shared__ float wsum[4];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int t = norm_row(blockIdx.x, a.T), tid = threadIdx.x;
     const int row = a.rows ? a.rows[t] : t;
     const int ng = a.D >> 2, nblk = a.D >> 5;
     float4 *h4 = (float4 *)(a.h + (size_t)row * a.D);
