@@ -416,11 +416,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
     if (c >= nchunks) return; // this token sees fewer keys
 
-    // ---- this wave's first query head, then the chunk's K and V rows
-    // (logical key -> cache slot), all loads in flight before the first store
+    // ---- the chunk's K and V rows (logical key -> cache slot), all loads in
+    // flight before the first store, then this wave's first query head
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
     const int nk = min(kDecKeys, limit - c * kDecKeys);
+    // issued before the RoPE work below, which they do not depend on
+    float4 kv[kDecLoads], vv[kDecLoads];
+#pragma unroll
+    for (int i = 0; i < kDecLoads; i++) {
+        const int e = tid + 256 * i; // float4 index in the kDecKeys x 32 chunk
+        const int key = min(e >> 5, nk - 1), d4 = e & 31;
+        const int kl = c * kDecKeys + key;
+        const int p = kl < n_sh ? slo + kl : seg + (kl - n_sh);
+        kv[i] = *(const float4 *)(kbase + (size_t)p * 128 + 4 * d4);
+        vv[i] = *(const float4 *)(vbase + (size_t)p * 128 + 4 * d4);
+    }
     // Fused RoPE + KV store (Rope.Apply, Rope.cs:112-135; ApplyPositionScale,
     // MinistralModel.cs:676-682; StoreKeys / StoreValues :649-669), the same
     // operations in the same order as rope_store_kernel: the projection's
@@ -485,16 +496,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     // workgroup forms it from the partials and stores it to the cache
     const bool own_chunk = a.rope_fused && c == nchunks - 1;
     {
-        float4 kv[kDecLoads], vv[kDecLoads];
-#pragma unroll
-        for (int i = 0; i < kDecLoads; i++) {
-            const int e = tid + 256 * i; // float4 index in the kDecKeys x 32 chunk
-            const int key = min(e >> 5, nk - 1), d4 = e & 31;
-            const int kl = c * kDecKeys + key;
-            const int p = kl < n_sh ? slo + kl : seg + (kl - n_sh);
-            kv[i] = *(const float4 *)(kbase + (size_t)p * 128 + 4 * d4);
-            vv[i] = *(const float4 *)(vbase + (size_t)p * 128 + 4 * d4);
-        }
 #pragma unroll
         for (int i = 0; i < kDecLoads; i++) {
             const int e = tid + 256 * i;
