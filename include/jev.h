@@ -152,13 +152,21 @@ int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tok
 int jev_margins(const float *verdicts, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature,
                 float *margins, float *probs);
 
-/* ParallelOptions.CancellationToken: polled between layers; the forward in
- * flight returns JEV_ECANCELED and the flag clears. */
+/* ParallelOptions.CancellationToken (MinistralModel.cs:301-304, KernelTests.cs:206-219):
+ * cancels the call in flight on ctx -- jev_forward, jev_forward_tree,
+ * jev_decode_greedy, jev_capture -- which then returns JEV_ECANCELED with the
+ * cache length unchanged (greedy decoding: advanced by the steps that ran).
+ * Those calls keep at most two layers (decode: two steps) enqueued ahead of
+ * the device and check between them, so the work stops within that many
+ * layers; a cancel that lands after the last layer was enqueued still cancels
+ * the call.  A cancel aimed at no call (none in flight) does nothing, so it
+ * never reaches a later call.  The only entry point safe from another thread. */
 void jev_cancel(jev_ctx *ctx);
 
 /* Timing support: device-resident variant of jev_forward for a fixed plan.
  * d_tokens / d_out are device pointers; the call only enqueues work on the
- * context's stream (no host synchronisation); jev_sync waits for it. */
+ * context's stream (no host synchronisation); jev_sync waits for it.  A
+ * cancel is honoured only while it enqueues (between layers). */
 int jev_forward_device(jev_ctx *ctx, const int32_t *d_tokens, int32_t n_tokens, const jev_layout *layout, int mode,
                        const int32_t *rows, int32_t n_rows, float *d_out);
 int jev_sync(jev_ctx *ctx);
@@ -207,6 +215,12 @@ int jev_set_matmul_strategy(int strategy);
 int jev_get_matmul_strategy(void);
 
 /* ---- Test hooks (no managed counterpart) ---- */
+
+/* The Rope ctor's tables (Rope.cs:33-106): the n = rope_dim / 2 pair
+ * frequencies (YaRN-ramped when ModelConfig.YarnActive, ModelConfig.cs:54-56)
+ * and the magnitude scale folded into cos / sin (ComputeMagnitudeScale,
+ * Rope.cs:78-88) -- the tables jev_create uploads.  Host only: no device. */
+int jev_rope_table(const jev_config *cfg, float *freqs, int32_t n, float *mscale);
 
 /* Dequantizer.Dequantize (Dequantizer.cs:45-93) run on the device:
  * `count` elements from GGUF blocks to float32. */

@@ -788,12 +788,6 @@ template <int TYPE, int MODE>
 static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
 {
     // Shape choice by M only changes which rows share a tile, never a result bit.
-#ifdef JEV_GEMM_CFG
-    return JEV_GEMM_CFG(a, s);
-#endif
-#ifdef JEV_GEMM_BD
-    return JEV_GEMM_BD(a, s);
-#endif
     // Measured on MI355X (3B shapes, Q8_0): small batches take B-direct
     // 32 x 128 tiles (4-5 % ahead of dequant-in-LDS 64 x 64 tiles on the
     // store shapes), large batches B-direct 64 x 256 tiles.  B-direct needs

@@ -81,6 +81,7 @@ struct DevBuf {
 
 struct Layer {
     float *attn_norm = nullptr, *ffn_norm = nullptr;
+    int64_t attn_norm_n = 0, ffn_norm_n = 0; // elements bound
     QWeight q, k, v, o, gate, up, down;
 };
 
@@ -100,12 +101,21 @@ struct jev_ctx {
     hipStream_t stream = nullptr;
     QWeight embd, output;
     float *out_norm = nullptr;
+    int64_t out_norm_n = 0;
     std::vector<Layer> layers;
     float *freqs = nullptr;
     int half = 0;
     float mscale = 1.f;
     bool finalized = false;
-    std::atomic<int> cancel{0};
+    // Cancellation (ParallelOptions.CancellationToken): `active` is the id of
+    // the call in flight (0 when idle); jev_cancel marks that id, so a cancel
+    // never outlives the call it was aimed at.
+    std::atomic<uint64_t> active{0}, cancel_id{0};
+    uint64_t calls = 0;
+    // One event per layer in flight: the host stays at most kLeadLayers layers
+    // ahead of the device so that a cancel stops the work within that many layers.
+    static constexpr int kLayerEvents = 4, kLeadLayers = 2;
+    hipEvent_t layer_ev[kLayerEvents] = {};
 
     // KV arena: fp32 K and V (the cache's contents) and their fp16-pair
     // shadows (same byte size; [layer][kv head][cap][hi, lo][hd]) that the
@@ -117,7 +127,7 @@ struct jev_ctx {
     // workspace
     DevBuf<float> h, y, yo, ydown, q, x32, f32, xn, logits, part, xsum;
     DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
-    DevBuf<int32_t> ints;
+    DevBuf<int32_t> ints, dec_state;
     DevBuf<AttnTile> tiles;
     DevBuf<float> amax_v;
     DevBuf<int32_t> amax_i;
@@ -232,6 +242,15 @@ struct ProfScope {
         }
         return c->ev_pool[c->ev_used++];
     }
+};
+
+// Marks one cancellable call in flight on a context.
+struct CallScope {
+    jev_ctx *c;
+    uint64_t id;
+    explicit CallScope(jev_ctx *ctx) : c(ctx), id(++ctx->calls) { c->active.store(id); }
+    ~CallScope() { c->active.store(0); }
+    bool cancelled() const { return c->cancel_id.load() == id; }
 };
 
 double weight_bytes(const QWeight &w) { return (double)row_bytes(w.type, w.cols) * w.rows; }
@@ -551,7 +570,12 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
 
 // Enqueues the whole forward pass; the head output lands in `dout`
 // (device) or in ctx->logits / ctx->xn scratch.
-int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout, const int32_t *dpos = nullptr)
+// `call` (optional) is the cancellable call this pass belongs to: its cancel
+// flag is checked before every layer; with `throttle` the host also waits
+// until the device has finished the layer kLeadLayers back before enqueuing
+// the next, so a cancel stops the pass within that many layers.
+int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout, const int32_t *dpos = nullptr,
+                    const CallScope *call = nullptr, bool throttle = false)
 {
     const jev_config &f = c->cfg;
     const int T = p.T, D = f.hidden, qdim = c->qdim(), kvdim = c->kvdim();
@@ -565,7 +589,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     const size_t stride_d = (size_t)T * D; // floats between partials of yo / ydown
     HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
     for (int l = 0; l < f.n_layers; l++) {
-        if (c->cancel.exchange(0)) return fail(JEV_ECANCELED, "the forward pass was cancelled at layer %d", l);
+        if (call && throttle && l >= jev_ctx::kLeadLayers)
+            HIP_TRY(hipEventSynchronize(c->layer_ev[(l - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]));
+        if (call && call->cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled at layer %d", l);
         const Layer &L = c->layers[l];
         float *kc = c->kc + (size_t)l * c->layer_stride();
         float *vc = c->vc + (size_t)l * c->layer_stride();
@@ -749,6 +775,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
             if (rc) return rc;
         }
+        if (call && throttle) HIP_TRY(hipEventRecord(c->layer_ev[l % jev_ctx::kLayerEvents], s));
     }
 
     // Heads.  The last layer's FFN residual is folded into the final norm of
@@ -900,6 +927,8 @@ int jev_create(const jev_config *cfg, int device, jev_ctx **out)
         return fail(JEV_EDEVICE, "hipStreamCreate: %s", hipGetErrorString(e));
     }
     e = hipEventCreateWithFlags(&c->copied, hipEventDisableTiming);
+    for (int i = 0; i < jev_ctx::kLayerEvents && e == hipSuccess; i++)
+        e = hipEventCreateWithFlags(&c->layer_ev[i], hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventRecord(c->copied, c->stream);
     if (e != hipSuccess) {
         jev_destroy(c);
@@ -944,10 +973,12 @@ void jev_destroy(jev_ctx *c)
     if (c->vp) (void)hipFree(c->vp);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->f32.release(); c->xn.release(); c->logits.release();
-    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->dec_state.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
     if (c->copied) (void)hipEventDestroy(c->copied);
+    for (auto e : c->layer_ev)
+        if (e) (void)hipEventDestroy(e);
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -974,7 +1005,12 @@ int jev_bind_tensor(jev_ctx *c, int slot, int layer, int type, int64_t rows, int
         if (rows != 1) return fail(JEV_EDATA, "a norm weight must be 1-D");
         float **dst = slot == JEV_SLOT_OUTPUT_NORM ? &c->out_norm
                     : slot == JEV_SLOT_ATTN_NORM ? &c->layers[layer].attn_norm : &c->layers[layer].ffn_norm;
-        return upload_vector(type, cols, bytes, dst);
+        int64_t *dn = slot == JEV_SLOT_OUTPUT_NORM ? &c->out_norm_n
+                    : slot == JEV_SLOT_ATTN_NORM ? &c->layers[layer].attn_norm_n : &c->layers[layer].ffn_norm_n;
+        *dn = 0;
+        int rc = upload_vector(type, cols, bytes, dst);
+        if (rc == JEV_OK) *dn = cols;
+        return rc;
     }
     if (!is_quant(type)) return fail(JEV_EDATA, "weight matrices must be Q8_0, Q5_1 or Q4_0 (type %d)", type);
     QWeight *w = nullptr;
@@ -1006,12 +1042,23 @@ int jev_finalize(jev_ctx *c)
         return fail(JEV_EDATA, "token_embd is %d wide but the model's hidden size is %d.", c->embd.cols, f.hidden);
     if (c->table().rows != f.vocab || c->table().cols != f.hidden)
         return fail(JEV_EDATA, "the LM head is %d x %d; expected %d x %d", c->table().rows, c->table().cols, f.vocab, f.hidden);
+    // Greedy decoding feeds argmax ids (< vocab) back into the embedding
+    // gather on the device, so the table must hold every vocabulary row.
+    if (c->embd.rows < f.vocab)
+        return fail(JEV_EDATA, "token_embd has %d rows but the vocabulary has %d entries.", c->embd.rows, f.vocab);
+    // The norm kernels read `hidden` weights (Kernels.RmsNorm, Kernels.cs:25-60).
+    if (c->out_norm_n != f.hidden)
+        return fail(JEV_EDATA, "output_norm.weight has %lld elements; expected %d.", (long long)c->out_norm_n, f.hidden);
     for (int l = 0; l < f.n_layers; l++) {
         Layer &L = c->layers[l];
         const char *missing = !L.attn_norm ? "attn_norm" : !L.ffn_norm ? "ffn_norm" : !L.q.base ? "attn_q"
                             : !L.k.base ? "attn_k" : !L.v.base ? "attn_v" : !L.o.base ? "attn_output"
                             : !L.gate.base ? "ffn_gate" : !L.up.base ? "ffn_up" : !L.down.base ? "ffn_down" : nullptr;
         if (missing) return fail(JEV_EDATA, "missing tensor 'blk.%d.%s.weight'.", l, missing);
+        if (L.attn_norm_n != f.hidden || L.ffn_norm_n != f.hidden)
+            return fail(JEV_EDATA, "blk.%d.%s.weight has %lld elements; expected %d.", l,
+                        L.attn_norm_n != f.hidden ? "attn_norm" : "ffn_norm",
+                        (long long)(L.attn_norm_n != f.hidden ? L.attn_norm_n : L.ffn_norm_n), f.hidden);
         struct { const QWeight *w; int r, c; const char *n; } chk[] = {
             {&L.q, qdim, f.hidden, "attn_q"}, {&L.k, kvdim, f.hidden, "attn_k"}, {&L.v, kvdim, f.hidden, "attn_v"},
             {&L.o, f.hidden, qdim, "attn_output"}, {&L.gate, f.ffn, f.hidden, "ffn_gate"},
@@ -1113,6 +1160,7 @@ int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *
 {
     int rc = check_ready(c);
     if (rc) return rc;
+    CallScope call(c);
     Plan p;
     rc = prepare(c, tokens, false, T, layout, mode, rows, n_rows, p);
     if (rc) return rc;
@@ -1123,13 +1171,16 @@ int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *
         HIP_TRY(c->logits.ensure(std::max(c->logits.n, need)));
         dout = c->logits.p;
     }
-    rc = enqueue_forward(c, p, mode, n_rows, dout);
+    rc = enqueue_forward(c, p, mode, n_rows, dout, nullptr, &call, true);
     if (rc) {
         (void)hipStreamSynchronize(c->stream);
         return rc;
     }
     if (need) HIP_TRY(hipMemcpyAsync(out, dout, need * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
+    // a cancel that landed after the last layer was enqueued still cancels
+    // this call: the cache length stays where it was (KvCache.Advance is skipped)
+    if (call.cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled");
     c->len = std::max(c->len, p.end); // KvCache.Advance (MinistralModel.cs:360)
     return JEV_OK;
 }
@@ -1139,11 +1190,12 @@ int jev_forward_device(jev_ctx *c, const int32_t *d_tokens, int32_t T, const jev
 {
     int rc = check_ready(c);
     if (rc) return rc;
+    CallScope call(c);
     Plan p;
     rc = prepare(c, d_tokens, true, T, layout, mode, rows, n_rows, p);
     if (rc) return rc;
     if (out_floats(c, mode, p.n_out, n_rows) && !d_out) return fail(JEV_EINVAL, "d_out is null");
-    rc = enqueue_forward(c, p, mode, n_rows, d_out);
+    rc = enqueue_forward(c, p, mode, n_rows, d_out, nullptr, &call, false);
     if (rc) return rc;
     c->len = std::max(c->len, p.end);
     return JEV_OK;
@@ -1200,6 +1252,7 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     if (rc) return rc;
     if (n_steps <= 0 || !tokens_out) return fail(JEV_EINVAL, "bad arguments");
     if (first < 0 || first >= c->embd.rows) return fail(JEV_EINVAL, "Token id %d is outside the embedding table.", first);
+    CallScope call(c);
     // Every step is the same launch sequence: the token, the cache length and
     // the output index live in device memory (state = {length, step, token})
     // and the argmax kernel advances them.  The step is captured once as a
@@ -1208,9 +1261,8 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     const int start = c->len, end = start + n_steps;
     rc = kv_ensure(c, end);
     if (rc) return rc;
-    DevBuf<int32_t> st;
-    HIP_TRY(st.ensure((size_t)n_steps + 3));
-    int32_t *state = st.p, *out = st.p + 3;
+    HIP_TRY(c->dec_state.ensure((size_t)n_steps + 3));
+    int32_t *state = c->dec_state.p, *out = c->dec_state.p + 3;
     const int32_t init[3] = {start, 0, first};
     HIP_TRY(hipMemcpy(state, init, sizeof(init), hipMemcpyHostToDevice));
     Plan p;
@@ -1238,29 +1290,46 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
         if (!rc && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
             rc = fail(JEV_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
     }
-    int done = 0;
-    for (; !rc && done < n_steps; done++) {
-        if (c->cancel.exchange(0)) {
-            rc = fail(JEV_ECANCELED, "greedy decoding was cancelled after %d steps", done);
+    // Steps are enqueued at most kLeadLayers ahead of the device (one event
+    // per step), so a cancel stops the loop within that many steps.
+    int launched = 0;
+    while (!rc && launched < n_steps) {
+        if (launched >= jev_ctx::kLeadLayers) {
+            hipError_t e = hipEventSynchronize(c->layer_ev[(launched - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]);
+            if (e != hipSuccess) {
+                rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+                break;
+            }
+        }
+        if (call.cancelled()) {
+            rc = fail(JEV_ECANCELED, "greedy decoding was cancelled after %d steps", launched);
             break;
         }
         if (exec) {
             hipError_t e = hipGraphLaunch(exec, c->stream);
-            if (e != hipSuccess) rc = fail(JEV_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+            if (e != hipSuccess) {
+                rc = fail(JEV_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+                break;
+            }
         } else {
             rc = step();
+            if (rc) break;
         }
+        launched++;
+        hipError_t e = hipEventRecord(c->layer_ev[(launched - 1) % jev_ctx::kLayerEvents], c->stream);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
     }
     hipError_t e = hipStreamSynchronize(c->stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
-    c->len = std::max(c->len, start + done - (rc && rc != JEV_ECANCELED ? 1 : 0));
+    if (!rc && call.cancelled()) rc = fail(JEV_ECANCELED, "greedy decoding was cancelled after %d steps", launched);
+    // every launched step ran to the end and advanced the cache by one token
+    if (!rc || rc == JEV_ECANCELED) c->len = std::max(c->len, start + launched);
     if (!rc) {
         e = hipMemcpy(tokens_out, out, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
     }
-    st.release();
     return rc;
 }
 
@@ -1328,7 +1397,9 @@ int jev_profile_read(jev_ctx *c, int cls, int64_t *launches, double *total_ms, d
 
 void jev_cancel(jev_ctx *c)
 {
-    if (c) c->cancel.store(1);
+    if (!c) return;
+    const uint64_t a = c->active.load();
+    if (a) c->cancel_id.store(a); // aimed at the call in flight; none in flight: nothing to cancel
 }
 
 // ---------------------------------------------------------------- test hooks
@@ -1392,6 +1463,19 @@ int jev_quantize_activations(const float *x, int64_t count, void *out, size_t ou
         }
         if (block_sums) block_sums[b] = sums[(size_t)b * 16];
     }
+    return JEV_OK;
+}
+
+int jev_rope_table(const jev_config *cfg, float *freqs, int32_t n, float *mscale)
+{
+    if (!cfg || !freqs || !mscale) return fail(JEV_EINVAL, "null argument");
+    if (cfg->rope_dim <= 0 || cfg->rope_dim % 2 != 0) return fail(JEV_EINVAL, "rope_dim %d must be even and positive", cfg->rope_dim);
+    if (n != cfg->rope_dim / 2) return fail(JEV_EINVAL, "the table has %d entries; %d given", cfg->rope_dim / 2, n);
+    std::vector<float> f;
+    float m = 1.f;
+    rope_table(*cfg, f, m);
+    std::copy(f.begin(), f.end(), freqs);
+    *mscale = m;
     return JEV_OK;
 }
 

@@ -353,3 +353,12 @@ def margins(verdicts, n_yes: int, n_no: int, temperature: float = 1.0):
     L.check(L.lib().jev_margins(_ptr(v, ctypes.c_float), len(v), n_yes, n_no, temperature,
                                 _ptr(m, ctypes.c_float), _ptr(p, ctypes.c_float)))
     return m, p
+
+
+def rope_table(config: ModelConfig):
+    """The Rope ctor's frequency table and magnitude scale (Rope.cs:33-106), as the library uploads them."""
+    n = config.rope_dim // 2
+    f = np.empty(n, np.float32)
+    m = ctypes.c_float()
+    L.check(L.lib().jev_rope_table(ctypes.byref(config.to_c()), _ptr(f, ctypes.c_float), n, ctypes.byref(m)))
+    return f, float(m.value)

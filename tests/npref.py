@@ -25,12 +25,74 @@ def rmsnorm(x, w, eps):
     return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
 
 
+def yarn_active(cfg) -> bool:
+    """ModelConfig.YarnActive (ModelConfig.cs:54-56)."""
+    return bool(cfg.rope_scaling_yarn) and cfg.rope_original_context > 0 and cfg.yarn_ext_factor != 0 \
+        and cfg.rope_scale_factor > 1
+
+
+def rope_tables(cfg):
+    """Rotary frequencies and magnitude scale in float64, from YaRN's definition
+    (Peng et al. 2023, "YaRN: Efficient Context Window Extension of Large Language
+    Models", sec. 3.2-3.4) in the form ggml implements it.
+
+    Pair i turns at theta_i = base^(-2i/d).  Over the original window of L
+    tokens it makes r(i) = L * theta_i / (2 pi) turns.  Pairs that turn at
+    least beta_fast times keep theta_i (extrapolation), pairs that turn at most
+    beta_slow times take theta_i / s (interpolation), and the pairs between
+    blend the two on a ramp that is linear in the pair index, between
+    floor(i_fast) and ceil(i_slow), where r(i_fast) = beta_fast and
+    r(i_slow) = beta_slow (found here by root-finding on r, not by the closed
+    form).  ext_factor scales the extrapolated share.  The attention
+    magnitude factor is 1 + 0.1 m ln s (sec. 3.4), taken as the ratio of the
+    "mscale" and "mscale_all_dim" variants when the latter is stored, times
+    the checkpoint's attention factor.  Without YaRN every pair is theta_i / s
+    and the magnitude is the attention factor alone."""
+    from scipy.optimize import brentq
+
+    d, base, s = cfg.rope_dim, np.float64(cfg.rope_freq_base), np.float64(cfg.rope_scale_factor)
+    i = np.arange(d // 2, dtype=np.float64)
+    theta = base ** (-2.0 * i / d)
+    if not yarn_active(cfg):
+        return theta / s, np.float64(cfg.rope_attn_factor)
+    L = np.float64(cfg.rope_original_context)
+
+    def log_turns(x):  # ln r(x), so the bracket below never overflows
+        return np.log(L) - 2.0 * x / d * np.log(base) - np.log(2.0 * np.pi)
+
+    if cfg.yarn_beta_fast == 0 and cfg.yarn_beta_slow == 0:
+        low, high = np.float64(np.finfo(np.float32).max), d / 2.0 - 1.0
+    else:
+        root = lambda beta: brentq(lambda x: log_turns(x) - np.log(beta), -1e4, 1e4, xtol=1e-12)
+        low = max(0.0, np.floor(root(np.float64(cfg.yarn_beta_fast))))
+        high = min(d / 2.0 - 1.0, np.ceil(root(np.float64(cfg.yarn_beta_slow))))
+    ramp = np.clip((i - low) / max(0.001, high - low), 0.0, 1.0)
+    mix = (1.0 - ramp) * cfg.yarn_ext_factor
+    freqs = theta / s * (1.0 - mix) + theta * mix
+
+    def magnitude(m):
+        return 1.0 if s <= 1 else 1.0 + 0.1 * m * np.log(s)
+
+    m = cfg.yarn_mscale if cfg.yarn_mscale != 0 else 1.0
+    ratio = magnitude(m) / magnitude(cfg.yarn_mscale_all_dim) if cfg.yarn_mscale_all_dim != 0 else magnitude(1.0)
+    return freqs, np.float64(ratio * cfg.rope_attn_factor)
+
+
+def position_scale(cfg, pos):
+    """Llama-4 attention temperature on the queries: 1 + beta ln(1 + floor(pos / n_orig))."""
+    pos = np.asarray(pos, np.float64)
+    if cfg.rope_original_context <= 0 or cfg.attention_temperature_scale == 0:
+        return np.ones_like(pos)
+    return 1.0 + np.float64(np.float32(cfg.attention_temperature_scale)) * np.log1p(
+        np.floor(pos / cfg.rope_original_context))
+
+
 def rope(x, pos, n_heads, cfg):
     hd = cfg.head_dim
-    freqs = 1.0 / np.power(np.float64(cfg.rope_freq_base), 2 * np.arange(cfg.rope_dim // 2) / cfg.rope_dim)
+    freqs, mscale = rope_tables(cfg)
     th = np.float32(pos)[:, None].astype(np.float32) * freqs.astype(np.float32)[None, :]  # float angle
     th = th.astype(np.float64)
-    c, s = np.cos(th), np.sin(th)
+    c, s = np.cos(th) * mscale, np.sin(th) * mscale
     x = x.reshape(len(pos), n_heads, hd).copy()
     x0, x1 = x[:, :, 0:cfg.rope_dim:2].copy(), x[:, :, 1:cfg.rope_dim:2].copy()
     x[:, :, 0:cfg.rope_dim:2] = x0 * c[:, None, :] - x1 * s[:, None, :]
@@ -48,7 +110,8 @@ def forward(cfg, W, tokens, positions, mask, out_rows):
     for l in range(cfg.n_layers):
         p = f"blk.{l}."
         x = rmsnorm(h, W[p + "attn_norm.weight"], cfg.rms_eps)
-        q = rope(x @ W[p + "attn_q.weight"].T, positions, H, cfg).reshape(T, H, hd)
+        q = rope(x @ W[p + "attn_q.weight"].T, positions, H, cfg) * position_scale(cfg, positions)[:, None]
+        q = q.reshape(T, H, hd)
         k = rope(x @ W[p + "attn_k.weight"].T, positions, KV, cfg).reshape(T, KV, hd)
         v = (x @ W[p + "attn_v.weight"].T).reshape(T, KV, hd)
         ctx = np.empty((T, H, hd))

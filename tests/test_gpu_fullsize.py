@@ -121,3 +121,49 @@ def test_full_shape_q5_1_greedy_decode_follows_oracle(gpu):
             nxt = int(tok)
     finally:
         ref.close()
+
+
+def _cancel_while_running(m, run):
+    import threading
+    import time
+    stop = threading.Event()
+
+    def spam():
+        while not stop.is_set():
+            m.cancel()
+            time.sleep(2e-4)
+
+    t = threading.Thread(target=spam)
+    t.start()
+    try:
+        return run()
+    finally:
+        stop.set()
+        t.join()
+
+
+def test_full_shape_cancel_reaches_a_prefill_and_a_decode_in_flight(model):
+    """OperationCanceledException's contract (KernelTests.cs:206-219) at the 3B shape: another
+    thread cancels a 4096-token prefill (~60 ms on the device) and a 64-step greedy decode while
+    they run; each returns cancelled, the prefill leaves the cache length unchanged, the decode
+    keeps the steps that ran, and the next call gives the same bits as an uncancelled run."""
+    import time
+    tokens = jev.random_tokens(4096, VOCAB, 31)
+    model.reset_kv_cache()
+    want = model.forward(tokens[:64])
+    model.reset_kv_cache()
+    t0 = time.perf_counter()
+    with pytest.raises(jev.CancelledError):
+        _cancel_while_running(model, lambda: model.prefill(tokens))
+    took = time.perf_counter() - t0
+    assert model.cached_token_count == 0
+    assert np.array_equal(model.forward(tokens[:64]), want)
+    model.reset_kv_cache()
+    model.prefill(tokens[:32])
+    with pytest.raises(jev.CancelledError):
+        _cancel_while_running(model, lambda: model.decode_greedy(int(tokens[31]), 64))
+    assert 32 <= model.cached_token_count < 32 + 64
+    model.cancel()  # aimed at no call
+    model.reset_kv_cache()
+    assert np.array_equal(model.forward(tokens[:64]), want)
+    print(f"cancelled 4096-token prefill returned after {took * 1e3:.1f} ms", flush=True)

@@ -13,6 +13,7 @@ import pytest
 
 import jev
 from helpers import rel_l2, tiny_config, worst_close
+from jev._lib import SLOT_OUTPUT
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -255,14 +256,51 @@ def test_errors_match_reference_exceptions(model):
     assert m.cached_token_count == 0
 
 
-def test_cancel_between_layers(model):
+def test_cancel_aimed_at_no_call_does_not_reach_the_next_one(model):
+    # A token cancelled between calls cancels nothing the library runs: the
+    # next call (any entry point) completes.
     m = fresh(model)
     m.cancel()
-    with pytest.raises(jev.CancelledError):
-        m.forward([1, 2, 3])
-    assert m.cached_token_count == 0
-    m.forward([1, 2, 3])  # the flag clears
+    m.forward([1, 2, 3])
     assert m.cached_token_count == 3
+    m.cancel()
+    m.decode_greedy(5, 2)
+    assert m.cached_token_count == 5
+    m.cancel()
+    m.forward_branches([[7], [8, 9]], ROWS)
+
+
+def cancel_while_running(m, run):
+    """Runs `run()` while another thread cancels m's call in flight every 0.2 ms
+    until it returns (ctypes releases the GIL during the library call)."""
+    import threading
+    import time
+    stop = threading.Event()
+
+    def spam():
+        while not stop.is_set():
+            m.cancel()
+            time.sleep(2e-4)
+
+    t = threading.Thread(target=spam)
+    t.start()
+    try:
+        return run()
+    finally:
+        stop.set()
+        t.join()
+
+
+def test_cancel_in_flight_leaves_the_cache_and_the_next_call_intact(model):
+    tokens = jev.random_tokens(4000, 2048, 23)
+    want = fresh(model).forward(tokens[:500])
+    m = fresh(model)
+    m.prefill(tokens[:100])
+    with pytest.raises(jev.CancelledError):
+        cancel_while_running(m, lambda: m.prefill(tokens[100:]))
+    assert m.cached_token_count == 100
+    got = m.forward(tokens[100:500])  # continues the 100 cached tokens
+    assert np.array_equal(got, want)
 
 
 def test_finalize_requires_every_tensor(gpu, synth):
@@ -274,6 +312,39 @@ def test_finalize_requires_every_tensor(gpu, synth):
     t = synth.tensors["token_embd.weight"]
     with pytest.raises(jev.DataError):
         m.bind(t.slot, t.layer, t.ggml_type, t.rows, t.cols, t.data[:-1])  # truncated
+    m.close()
+
+
+@pytest.mark.parametrize("name", ["output_norm.weight", "blk.1.attn_norm.weight", "blk.0.ffn_norm.weight"])
+def test_finalize_rejects_a_short_norm(gpu, synth, name):
+    """A norm shorter than `hidden` would be read past its end by the norm kernel: finalize
+    refuses it by name (InvalidDataException's role) before any kernel runs."""
+    m = jev.MinistralModel(synth.config)
+    for n, t in synth.tensors.items():
+        if n == name:
+            short = t.data[: (t.cols - 32) * 4]
+            m.bind(t.slot, t.layer, t.ggml_type, 1, t.cols - 32, short)
+        else:
+            m.bind(t.slot, t.layer, t.ggml_type, t.rows, t.cols, t.data)
+    with pytest.raises(jev.DataError, match=name.replace(".weight", "")):
+        m.finalize()
+    m.close()
+
+
+def test_finalize_rejects_an_embedding_table_shorter_than_the_vocabulary(gpu, synth):
+    """With an untied output head, greedy decoding still feeds argmax ids (< vocab) to the
+    embedding gather, so token_embd must hold every vocabulary row."""
+    c = synth.config
+    m = jev.MinistralModel(c)
+    for n, t in synth.tensors.items():
+        if n == "token_embd.weight":
+            keep = c.vocab - 16
+            m.bind(t.slot, t.layer, t.ggml_type, keep, t.cols, t.data[: keep * (t.data.size // t.rows)])
+            m.bind(SLOT_OUTPUT, 0, t.ggml_type, t.rows, t.cols, t.data)
+        else:
+            m.bind(t.slot, t.layer, t.ggml_type, t.rows, t.cols, t.data)
+    with pytest.raises(jev.DataError, match="token_embd"):
+        m.finalize()
     m.close()
 
 
