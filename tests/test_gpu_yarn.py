@@ -90,7 +90,14 @@ def test_tree_verdicts_and_bitwise_contract(model, ref):
     m.prefill(trunk)
     for b, br in enumerate(branches):
         m.kv_truncate(len(trunk))
-        assert np.array_equal(m.forward_selected(br, ROWS), g[b]), b
+        alone = m.forward_selected(br, ROWS)
+        if len(br) >= 2:
+            assert np.array_equal(alone, g[b]), b
+        else:
+            # one token alone takes the one-token (row-dot) path, as the reference
+            # dispatches below PanelMinTokens = 2 (QuantMatMul.cs:51, :84): the
+            # tolerance applies, not the bitwise contract
+            assert worst_close(g[b], alone) <= 1e-3, b
 
 
 def test_greedy_decode_graph_follows_oracle(model, ref):
