@@ -201,6 +201,17 @@ void jev_weight_destroy(jev_weight *w);
  * pointers; tokens >= 2 take the MFMA GEMM, 1 token the GEMV (the dispatch of
  * QuantMatMul.cs:84-101).  Only enqueues on the weight's stream. */
 int jev_matmul_device(jev_weight *w, const float *x, int32_t tokens, float *y);
+/* jev_matmul_device without any allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory during the call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same kernels and the same result bits as jev_matmul_device;
+ * the call's scratch (fp16 pair of x, Q5_1 block sums, K-split partials, or
+ * the integer strategy's quantized activations) comes from one static 16 MiB
+ * device array per GPU, held until the process ends.  A call whose scratch
+ * would exceed 16 MiB fails with JEV_EINVAL (256 tokens x 3072 x 3072 fits).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (on different weights' streams, or from several threads) race. */
+int jev_matmul_device_noalloc(jev_weight *w, const float *x, int32_t tokens, float *y);
 int jev_weight_sync(jev_weight *w);
 
 /* QuantMatMul.Strategy (QuantMatMul.cs:10-41), process-wide, read by every

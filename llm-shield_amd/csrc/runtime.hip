@@ -14,6 +14,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -1509,39 +1510,106 @@ struct jev_weight {
     DevBuf<int> xqs;
 };
 
+// Device buffers one matmul call works in (besides x and y).
+struct MatmulBufs {
+    uint16_t *xt = nullptr; // fp16 pair of x, operand-tile layout (tokens >= 2)
+    float *xsum = nullptr;  // Q5_1: per-32 block sums of x
+    float *part = nullptr;  // K-split partials (ksplit > 1)
+    int8_t *xq = nullptr;   // integer strategy: quantized activations and their block data
+    float *xd = nullptr, *xs = nullptr;
+    int *xqs = nullptr;
+};
+// Bytes of each buffer a call of `tokens` rows needs, in MatmulBufs order.
+struct MatmulNeeds {
+    size_t xt = 0, xsum = 0, part = 0, xq = 0, xd = 0, xs = 0, xqs = 0;
+    int ksplit = 1;
+    bool integer = false;
+};
+static MatmulNeeds matmul_needs(const QWeight &w, int tokens, bool integer)
+{
+    MatmulNeeds n;
+    const size_t t16 = ((size_t)tokens + 15) & ~(size_t)15, nb = (size_t)w.cols / 32;
+    n.integer = integer;
+    if (integer) {
+        n.xq = t16 * w.cols;
+        n.xd = n.xs = n.xqs = nb * t16 * 4;
+        return n;
+    }
+    n.ksplit = jev_ctx::split(tokens, w.rows, w.cols);
+    if (n.ksplit > 1) n.part = (size_t)tokens * w.rows * n.ksplit * sizeof(float);
+    if (tokens >= 2) {
+        n.xt = t16 * w.cols * 2 * sizeof(uint16_t);
+        if (w.type == kQ5_1) n.xsum = ((size_t)tokens * nb + 1) * sizeof(float);
+    }
+    return n;
+}
+
 // The Integer strategy on the device: quantize x [tokens][cols] (fp32, device)
 // to Q8_0 blocks, then the int8-MFMA block dots into y [tokens][rows].
-static hipError_t matmul_integer(const QWeight &w, const float *x, int tokens, float *y, DevBuf<int8_t> &xq,
-                                 DevBuf<float> &xd, DevBuf<int> &xqs, DevBuf<float> &xs, hipStream_t s)
+static hipError_t matmul_integer(const QWeight &w, const float *x, int tokens, float *y, const MatmulBufs &b,
+                                 hipStream_t s)
 {
-    const int t16 = (tokens + 15) & ~15, nb = w.cols / 32;
-    hipError_t e = xq.ensure((size_t)t16 * w.cols);
-    if (e == hipSuccess) e = xd.ensure((size_t)nb * t16);
-    if (e == hipSuccess) e = xqs.ensure((size_t)nb * t16);
-    if (e == hipSuccess) e = xs.ensure((size_t)nb * t16);
-    if (e != hipSuccess) return e;
+    const int t16 = (tokens + 15) & ~15;
     QuantActArgs q;
     q.x = x;
     q.T = tokens;
     q.K = w.cols;
     q.T16 = t16;
-    q.xq = xq.p;
-    q.xd = xd.p;
-    q.xqs = xqs.p;
-    q.xs = xs.p;
-    e = launch_quant_act(q, s);
+    q.xq = b.xq;
+    q.xd = b.xd;
+    q.xqs = b.xqs;
+    q.xs = b.xs;
+    hipError_t e = launch_quant_act(q, s);
     if (e != hipSuccess) return e;
     GemmI8Args g;
     g.w = w;
-    g.xq = xq.p;
-    g.xd = xd.p;
-    g.xqs = xqs.p;
-    g.xs = xs.p;
+    g.xq = b.xq;
+    g.xd = b.xd;
+    g.xqs = b.xqs;
+    g.xs = b.xs;
     g.T = tokens;
     g.T16 = t16;
     g.y = y;
     g.ldy = w.rows;
     return launch_gemm_i8(g, s);
+}
+
+// y = x . W^T on the device in the given buffers (QuantMatMul.ForwardAsync's
+// dispatch, QuantMatMul.cs:84-101): the integer strategy, else the MFMA GEMM
+// for two or more tokens and the GEMV for one, K-split partials summed after.
+static hipError_t matmul_run(const QWeight &w, const float *x, int tokens, float *y, const MatmulNeeds &n,
+                             const MatmulBufs &b, hipStream_t s)
+{
+    if (n.integer) return matmul_integer(w, x, tokens, y, b, s);
+    const int rows = w.rows, cols = w.cols;
+    float *dst = n.ksplit > 1 ? b.part : y;
+    hipError_t e = hipSuccess;
+    if (tokens >= 2) {
+        e = launch_split(x, tokens, cols, b.xt, s);
+        if (e == hipSuccess && w.type == kQ5_1) e = launch_block_sums(b.xt, tokens, cols, b.xsum, s);
+        if (e == hipSuccess) {
+            GemmArgs g;
+            g.M = tokens;
+            g.K = cols;
+            g.xt = b.xt;
+            g.xsum = b.xsum;
+            g.seg[0] = w;
+            g.ldy = rows;
+            g.y = dst;
+            g.ksplit = n.ksplit;
+            e = launch_gemm(g, s);
+        }
+    } else {
+        GemvArgs g;
+        g.K = cols;
+        g.x = x;
+        g.seg[0] = w;
+        g.y = dst;
+        g.ksplit = n.ksplit;
+        e = launch_gemv(g, s);
+    }
+    if (e == hipSuccess && n.ksplit > 1) e = launch_reduce_partials(dst, n.ksplit, tokens, rows, y, s);
+    return e;
 }
 
 int jev_weight_create(int type, int64_t rows, int64_t cols, const void *bytes, size_t nbytes, int device,
@@ -1593,46 +1661,95 @@ int jev_matmul_device(jev_weight *h, const float *x, int32_t tokens, float *y)
 {
     if (!h || !x || !y || tokens <= 0) return fail(JEV_EINVAL, "bad arguments");
     HIP_TRY(hipSetDevice(h->device));
-    const QWeight &w = h->w;
-    if (g_matmul_strategy.load() == JEV_MATMUL_INTEGER) {
-        HIP_TRY(matmul_integer(w, x, tokens, y, h->xq, h->xd, h->xqs, h->xs, h->stream));
-        return JEV_OK;
+    const MatmulNeeds n = matmul_needs(h->w, tokens, g_matmul_strategy.load() == JEV_MATMUL_INTEGER);
+    MatmulBufs b;
+    if (n.xt) HIP_TRY(h->xt.ensure(n.xt / sizeof(uint16_t)));
+    if (n.xsum) HIP_TRY(h->xsum.ensure(n.xsum / sizeof(float)));
+    if (n.part) HIP_TRY(h->part.ensure(n.part / sizeof(float)));
+    if (n.xq) HIP_TRY(h->xq.ensure(n.xq));
+    if (n.xd) HIP_TRY(h->xd.ensure(n.xd / sizeof(float)));
+    if (n.xs) HIP_TRY(h->xs.ensure(n.xs / sizeof(float)));
+    if (n.xqs) HIP_TRY(h->xqs.ensure(n.xqs / sizeof(int)));
+    b.xt = h->xt.p;
+    b.xsum = h->xsum.p;
+    b.part = h->part.p;
+    b.xq = h->xq.p;
+    b.xd = h->xd.p;
+    b.xs = h->xs.p;
+    b.xqs = h->xqs.p;
+    HIP_TRY(matmul_run(h->w, x, tokens, y, n, b, h->stream));
+    return JEV_OK;
+}
+
+// ---- The same matmul without allocation (jev_matmul_device_noalloc).
+//
+// Its buffers (the fp16 pair of x, Q5_1 block sums, K-split partials, or the
+// integer strategy's quantized activations) are carved from `scratch`, one
+// static device array per GPU that lives until the process ends.  Host code
+// never passes `scratch` itself to a kernel (that name is a host-side stand-in,
+// not a device address): the device address comes from hipGetSymbolAddress,
+// fetched once per device with that device current, and only that pointer is
+// used.  Nothing in it has to start at zero: every element a call reads was
+// written earlier in the same call (padding rows of the operand tiles feed
+// only padding outputs, which are never stored).
+} // extern "C"
+
+static constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_dev[kMaxDevices] = {};
+
+// The device address of this device's `scratch` (the current device must be `device`).
+int scratch_for(int device, uint8_t **out)
+{
+    if (device < 0 || device >= kMaxDevices) return fail(JEV_EINVAL, "device %d is out of range", device);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(JEV_EDEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+        g_scratch_dev[device] = (uint8_t *)p;
     }
-    const int rows = w.rows, cols = w.cols;
-    const int ksplit = jev_ctx::split(tokens, rows, cols);
-    float *dst = y;
-    if (ksplit > 1) {
-        HIP_TRY(h->part.ensure((size_t)tokens * rows * ksplit));
-        dst = h->part.p;
+    *out = g_scratch_dev[device];
+    return JEV_OK;
+}
+} // namespace
+
+extern "C" {
+
+int jev_matmul_device_noalloc(jev_weight *h, const float *x, int32_t tokens, float *y)
+{
+    if (!h || !x || !y || tokens <= 0) return fail(JEV_EINVAL, "bad arguments");
+    HIP_TRY(hipSetDevice(h->device));
+    const MatmulNeeds n = matmul_needs(h->w, tokens, g_matmul_strategy.load() == JEV_MATMUL_INTEGER);
+    // carve 256-byte aligned pieces in MatmulBufs order
+    const size_t sizes[7] = {n.xt, n.xsum, n.part, n.xq, n.xd, n.xs, n.xqs};
+    size_t off[7], total = 0;
+    for (int i = 0; i < 7; i++) {
+        off[i] = total;
+        total += (sizes[i] + 255) & ~(size_t)255;
     }
-    if (tokens >= 2) {
-        const size_t t16 = ((size_t)tokens + 15) & ~(size_t)15;
-        HIP_TRY(h->xt.ensure(t16 * cols * 2));
-        HIP_TRY(launch_split(x, tokens, cols, h->xt.p, h->stream));
-        if (w.type == kQ5_1) {
-            HIP_TRY(h->xsum.ensure((size_t)tokens * (cols / 32) + 1));
-            HIP_TRY(launch_block_sums(h->xt.p, tokens, cols, h->xsum.p, h->stream));
-        }
-        GemmArgs g;
-        g.M = tokens;
-        g.K = cols;
-        g.xt = h->xt.p;
-        g.xsum = h->xsum.p;
-        g.seg[0] = w;
-        g.ldy = rows;
-        g.y = dst;
-        g.ksplit = ksplit;
-        HIP_TRY(launch_gemm(g, h->stream));
-    } else {
-        GemvArgs g;
-        g.K = cols;
-        g.x = x;
-        g.seg[0] = w;
-        g.y = dst;
-        g.ksplit = ksplit;
-        HIP_TRY(launch_gemv(g, h->stream));
-    }
-    if (ksplit > 1) HIP_TRY(launch_reduce_partials(dst, ksplit, tokens, rows, y, h->stream));
+    if (total > kNoAllocScratchBytes)
+        return fail(JEV_EINVAL,
+                    "a %d-token matmul over a %d x %d weight needs %zu bytes of scratch; the no-allocation entry point "
+                    "has %zu (use jev_matmul_device)",
+                    tokens, h->w.rows, h->w.cols, total, kNoAllocScratchBytes);
+    uint8_t *base = nullptr;
+    int rc = scratch_for(h->device, &base);
+    if (rc) return rc;
+    MatmulBufs b;
+    b.xt = n.xt ? (uint16_t *)(base + off[0]) : nullptr;
+    b.xsum = n.xsum ? (float *)(base + off[1]) : nullptr;
+    b.part = n.part ? (float *)(base + off[2]) : nullptr;
+    b.xq = n.xq ? (int8_t *)(base + off[3]) : nullptr;
+    b.xd = n.xd ? (float *)(base + off[4]) : nullptr;
+    b.xs = n.xs ? (float *)(base + off[5]) : nullptr;
+    b.xqs = n.xqs ? (int *)(base + off[6]) : nullptr;
+    HIP_TRY(matmul_run(h->w, x, tokens, y, n, b, h->stream));
     return JEV_OK;
 }
 
@@ -1659,10 +1776,20 @@ int jev_matmul_q(int type, const void *wbytes, int64_t rows, int64_t cols, const
     if (e == hipSuccess) e = hipMalloc((void **)&dy, ny * ksplit * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(dx, x, nx * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess && g_matmul_strategy.load() == JEV_MATMUL_INTEGER) {
+        const MatmulNeeds n = matmul_needs(w, tokens, true);
         DevBuf<int8_t> xq;
         DevBuf<float> xd, xs;
         DevBuf<int> xqs;
-        e = matmul_integer(w, dx, tokens, dy, xq, xd, xqs, xs, nullptr);
+        e = xq.ensure(n.xq);
+        if (e == hipSuccess) e = xd.ensure(n.xd / sizeof(float));
+        if (e == hipSuccess) e = xs.ensure(n.xs / sizeof(float));
+        if (e == hipSuccess) e = xqs.ensure(n.xqs / sizeof(int));
+        MatmulBufs b;
+        b.xq = xq.p;
+        b.xd = xd.p;
+        b.xs = xs.p;
+        b.xqs = xqs.p;
+        if (e == hipSuccess) e = matmul_integer(w, dx, tokens, dy, b, nullptr);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         xq.release();
         xd.release();

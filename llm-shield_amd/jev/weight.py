@@ -35,6 +35,11 @@ class QuantWeight:
         """Enqueue y = x . W^T on the weight's stream (x, y: fp32 device pointers)."""
         L.check(self._lib.jev_matmul_device(self._h, ctypes.c_void_p(x_ptr), tokens, ctypes.c_void_p(y_ptr)))
 
+    def matmul_device_noalloc(self, x_ptr: int, tokens: int, y_ptr: int) -> None:
+        """matmul_device without allocation: the call's scratch is the library's
+        static 16 MiB device array (shared by every call on the GPU)."""
+        L.check(self._lib.jev_matmul_device_noalloc(self._h, ctypes.c_void_p(x_ptr), tokens, ctypes.c_void_p(y_ptr)))
+
     def sync(self) -> None:
         L.check(self._lib.jev_weight_sync(self._h))
 
