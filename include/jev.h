@@ -135,6 +135,22 @@ int jev_kv_restore(jev_ctx *ctx, const float *in, size_t n_floats, int32_t lengt
 int jev_forward(jev_ctx *ctx, const int32_t *tokens, int32_t n_tokens, const jev_layout *layout, int mode,
                 const int32_t *rows, int32_t n_rows, float *out, size_t out_len);
 
+/* IActivationSink.Observe (MinistralModel.cs:787-790): one named tensor of
+ * rows x columns floats, valid only during the call. */
+typedef void (*jev_sink)(void *user, const char *name, const float *values, int32_t rows, int32_t columns);
+
+/* The public ForwardAsync(tokens, capture, options) (MinistralModel.cs:157-160
+ * -> :301-435): appends `tokens` causally, writes the last token's vocab
+ * logits to `logits`, and calls `sink` once per tensor the reference observes,
+ * in its order and with its names -- "embeddings"; per layer l
+ * "blk.{l}.attn_norm", "q_rope", "k_rope", "v", "attn_weighted", "attn_out",
+ * "post_attn", "ffn_norm", "ffn_out", "output"; then "final_norm" and
+ * "logits" (MinistralModel.cs:331-357, :418-422, AttentionAsync :459-549).
+ * The sink runs on the calling thread after the pass has finished.  A
+ * debugging path: the device synchronises at every tap. */
+int jev_capture(jev_ctx *ctx, const int32_t *tokens, int32_t n_tokens, jev_sink sink, void *user, float *logits,
+                size_t out_len);
+
 /* ForwardTreeAsync (MinistralModel.cs:198-219): the trunk appended causally,
  * then every branch continuing from its end; branch_tokens holds the branches
  * back to back.  out = n_branches * n_rows verdict-row logits. */

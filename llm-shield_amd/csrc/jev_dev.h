@@ -62,7 +62,7 @@ __device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
 // 16 x 32 MFMA A-operand tile stored in lane order -- lane 16*(k%32 / 8) +
 // row%16 holds 8 consecutive k -- so a wave fetches its fragment with one
 // contiguous 1 KiB load.  part 0 = hi, 1 = lo.  Rows are padded to 16.
-__device__ __forceinline__ size_t xt_index(int row, int k, int nblk, int part)
+__host__ __device__ __forceinline__ size_t xt_index(int row, int k, int nblk, int part)
 {
     int rg = row >> 4, r = row & 15, b = k >> 5, kk = k & 31;
     return ((((size_t)rg * nblk + b) * 2 + part) * 64 + ((kk >> 3) * 16 + r)) * 8 + (kk & 7);

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "../../include/jev.h"
+#include "jev_dev.h"
 #include "jev_internal.h"
 
 using namespace jev;
@@ -126,7 +127,7 @@ struct jev_ctx {
     int cap = 0, len = 0;
 
     // workspace
-    DevBuf<float> h, y, yo, ydown, q, x32, f32, xn, logits, part, xsum;
+    DevBuf<float> h, y, yo, ydown, q, x32, f32, xn, logits, part, xsum, cap32;
     DevBuf<uint16_t> xt, ft; // fp16 pairs in the GEMM operand-tile layout
     DevBuf<int32_t> ints, dec_state;
     DevBuf<AttnTile> tiles;
@@ -571,13 +572,121 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
 
 // Enqueues the whole forward pass; the head output lands in `dout`
 // (device) or in ctx->logits / ctx->xn scratch.
+// ---- Activation capture (IActivationSink, MinistralModel.cs:787-790).
+//
+// jev_capture records every tensor the reference observes in ForwardAsync
+// (MinistralModel.cs:331-357, :418-422; AttentionAsync's q_rope, k_rope, v,
+// attn_weighted) as the device holds it: the stream is synchronised at each
+// tap and the tensor copied to the host.  K-split partials are summed in
+// split order (as their consumer sums them); k_rope and v are read back from
+// the cache rows the pass wrote; attn_weighted is rebuilt from the attention
+// output the O projection reads (the fp16 pair hi + lo, or, for one token,
+// the decode attention's chunks merged in ascending order).
+struct Capture {
+    struct Tap {
+        std::string name;
+        int rows, cols;
+        std::vector<float> v;
+    };
+    std::vector<Tap> taps;
+};
+
+int cap_add(jev_ctx *c, Capture *cap, std::string name, const float *d, int rows, int cols)
+{
+    Capture::Tap t{std::move(name), rows, cols, std::vector<float>((size_t)rows * cols)};
+    HIP_TRY(hipMemcpyAsync(t.v.data(), d, t.v.size() * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    cap->taps.push_back(std::move(t));
+    return JEV_OK;
+}
+
+// K-split partials (nsplit of them, rows * cols floats apart) summed in split order.
+int cap_partials(jev_ctx *c, Capture *cap, std::string name, const float *part, int nsplit, int rows, int cols)
+{
+    HIP_TRY(launch_reduce_partials(part, nsplit, rows, cols, c->cap32.p, c->stream));
+    return cap_add(c, cap, std::move(name), c->cap32.p, rows, cols);
+}
+
+// Rows [start, start + T) of every KV head of one layer's cache as [T][kv heads * hd].
+int cap_kv(jev_ctx *c, Capture *cap, std::string name, const float *layer, int start, int T)
+{
+    const int hd = c->cfg.head_dim, kvh = c->cfg.n_kv_heads;
+    Capture::Tap t{std::move(name), T, kvh * hd, std::vector<float>((size_t)T * kvh * hd)};
+    for (int h = 0; h < kvh; h++)
+        HIP_TRY(hipMemcpy2DAsync(t.v.data() + (size_t)h * hd, (size_t)kvh * hd * sizeof(float),
+                                 layer + ((size_t)h * c->cap + start) * hd, (size_t)hd * sizeof(float),
+                                 (size_t)hd * sizeof(float), T, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    cap->taps.push_back(std::move(t));
+    return JEV_OK;
+}
+
+// The attention output of T >= 2 tokens from its fp16 pair in the operand-tile layout.
+int cap_pair(jev_ctx *c, Capture *cap, std::string name, const uint16_t *xt, int T, int K)
+{
+    const size_t T16 = ((size_t)T + 15) & ~(size_t)15;
+    std::vector<uint16_t> raw(T16 * K * 2);
+    HIP_TRY(hipMemcpyAsync(raw.data(), xt, raw.size() * sizeof(uint16_t), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    Capture::Tap t{std::move(name), T, K, std::vector<float>((size_t)T * K)};
+    const int nblk = K >> 5;
+    for (int r = 0; r < T; r++)
+        for (int k = 0; k < K; k++)
+            t.v[(size_t)r * K + k] = half_to_float(raw[xt_index(r, k, nblk, 0)]) + half_to_float(raw[xt_index(r, k, nblk, 1)]);
+    cap->taps.push_back(std::move(t));
+    return JEV_OK;
+}
+
+// The one-token decode attention output from its per-chunk (max, sum, o[hd])
+// partials, merged in ascending chunk order with a running max, as the O
+// projection's GEMV merges them.
+int cap_chunks(jev_ctx *c, Capture *cap, std::string name, const float *part, int max_chunks, int nch)
+{
+    const int heads = c->cfg.n_heads, hd = c->cfg.head_dim, w = hd + 2;
+    std::vector<float> raw((size_t)heads * max_chunks * w);
+    HIP_TRY(hipMemcpyAsync(raw.data(), part, raw.size() * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    Capture::Tap t{std::move(name), 1, heads * hd, std::vector<float>((size_t)heads * hd)};
+    for (int h = 0; h < heads; h++) {
+        float M = -INFINITY, L = 0.f;
+        float *o = t.v.data() + (size_t)h * hd;
+        for (int ch = 0; ch < nch; ch++) {
+            const float *pc = raw.data() + ((size_t)h * max_chunks + ch) * w;
+            const float Mn = std::max(M, pc[0]), fo = expf(M - Mn), fc = expf(pc[0] - Mn);
+            L = fmaf(pc[1], fc, L * fo);
+            for (int d = 0; d < hd; d++) o[d] = fmaf(pc[2 + d], fc, o[d] * fo);
+            M = Mn;
+        }
+        for (int d = 0; d < hd; d++) o[d] = o[d] / L;
+    }
+    cap->taps.push_back(std::move(t));
+    return JEV_OK;
+}
+
+std::string layer_tap(int l, const char *tap)
+{
+    char b[64];
+    snprintf(b, sizeof b, "blk.%d.%s", l, tap);
+    return b;
+}
+
 // `call` (optional) is the cancellable call this pass belongs to: its cancel
 // flag is checked before every layer; with `throttle` the host also waits
 // until the device has finished the layer kLeadLayers back before enqueuing
 // the next, so a cancel stops the pass within that many layers.
+// With `cap` (a causal call of jev_capture) every tap is recorded as the pass
+// produces it; the one-token pass then runs RoPE before the decode attention
+// instead of inside it, so the rotated queries exist in memory.
 int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout, const int32_t *dpos = nullptr,
-                    const CallScope *call = nullptr, bool throttle = false)
+                    const CallScope *call = nullptr, bool throttle = false, Capture *cap = nullptr)
 {
+#define CAP_TRY(expr)                                                                                           \
+    do {                                                                                                        \
+        if (cap) {                                                                                              \
+            int rc_ = (expr);                                                                                   \
+            if (rc_) return rc_;                                                                                \
+        }                                                                                                       \
+    } while (0)
     const jev_config &f = c->cfg;
     const int T = p.T, D = f.hidden, qdim = c->qdim(), kvdim = c->kvdim();
     const int group = f.n_heads / f.n_kv_heads;
@@ -589,6 +698,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     const int s_o = c->split_o(T), s_down = c->split_down(T);
     const size_t stride_d = (size_t)T * D; // floats between partials of yo / ydown
     HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
+    CAP_TRY(cap_add(c, cap, "embeddings", c->h.p, T, D));
     for (int l = 0; l < f.n_layers; l++) {
         if (call && throttle && l >= jev_ctx::kLeadLayers)
             HIP_TRY(hipEventSynchronize(c->layer_ev[(l - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]));
@@ -613,8 +723,11 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         else {
             na.ot = c->xt.p;
             if (L.q.type == kQ5_1) na.xsum = c->xsum.p;
+            if (cap) na.out32 = c->cap32.p;
         }
         HIP_TRY(launch_rmsnorm(na, s));
+        if (l > 0) CAP_TRY(cap_add(c, cap, layer_tap(l - 1, "output"), c->h.p, T, D)); // h + the FFN residual
+        CAP_TRY(cap_add(c, cap, layer_tap(l, "attn_norm"), na.out32, T, D));
 
         // Q | K | V
         const int ldqkv = qdim + 2 * kvdim;
@@ -665,7 +778,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.orig_ctx = f.rope_original_context;
         ra.temp_scale = f.attention_temperature_scale;
         // one token: RoPE and the KV store run inside the decode attention kernel
-        if (T != 1) HIP_TRY(launch_rope_store(ra, s));
+        if (T != 1 || cap) HIP_TRY(launch_rope_store(ra, s));
+        CAP_TRY(cap_add(c, cap, layer_tap(l, "q_rope"), c->q.p, T, qdim));
+        CAP_TRY(cap_kv(c, cap, layer_tap(l, "k_rope"), kc, p.start, T));
+        CAP_TRY(cap_kv(c, cap, layer_tap(l, "v"), vc, p.start, T));
         DecodeChunks dchunks;
 
         if (T == 1) {
@@ -687,7 +803,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.start_dev = dpos;
             da.scale = scale;
             da.part = c->part.p;
-            da.rope_fused = 1;
+            da.rope_fused = cap ? 0 : 1;
             da.rope = ra;
             // the O GEMV merges the chunks while staging its input
             dchunks.part = da.part;
@@ -701,6 +817,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
                          8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
             HIP_TRY(launch_attn_decode(da, s));
+            CAP_TRY(cap_chunks(c, cap, layer_tap(l, "attn_weighted"), c->part.p, p.max_chunks,
+                               (p.start + 1 + kDecodeKeys - 1) / kDecodeKeys));
         } else {
             AttnArgs aa;
             aa.n_tiles = p.n_tiles;
@@ -719,6 +837,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
                              8.0 * f.head_dim * f.n_kv_heads * p.kv_rows + 8.0 * T * qdim);
                 HIP_TRY(launch_attn_tree(aa, s));
             }
+            CAP_TRY(cap_pair(c, cap, layer_tap(l, "attn_weighted"), c->xt.p, T, qdim));
             if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xt.p, T, qdim, c->xsum.p, s));
         }
         {
@@ -727,6 +846,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
                             T == 1 ? &dchunks : nullptr);
             if (rc) return rc;
         }
+        CAP_TRY(cap_partials(c, cap, layer_tap(l, "attn_out"), c->yo.p, s_o, T, D));
 
         // FFN norm (+ attention residual)
         NormArgs nf = na;
@@ -735,6 +855,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         nf.w = L.ffn_norm;
         nf.xsum = (T > 1 && L.gate.type == kQ5_1) ? c->xsum.p : nullptr;
         HIP_TRY(launch_rmsnorm(nf, s));
+        CAP_TRY(cap_add(c, cap, layer_tap(l, "post_attn"), c->h.p, T, D));
+        CAP_TRY(cap_add(c, cap, layer_tap(l, "ffn_norm"), nf.out32, T, D));
 
         const bool gu_rows = T == 1 && L.gate.type == L.up.type && f.ffn % 16 == 0;
         if (gu_rows) {
@@ -776,6 +898,15 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
             if (rc) return rc;
         }
+        CAP_TRY(cap_partials(c, cap, layer_tap(l, "ffn_out"), c->ydown.p, s_down, T, D));
+        if (cap && l == f.n_layers - 1) {
+            // the last layer's residual is folded into the final norm of the
+            // output rows; h + ffn_out is that same single fp32 add
+            const std::vector<float> &hp = cap->taps[cap->taps.size() - 3].v; // post_attn
+            Capture::Tap o{layer_tap(l, "output"), T, D, cap->taps.back().v};
+            for (size_t i = 0; i < o.v.size(); i++) o.v[i] = hp[i] + o.v[i];
+            cap->taps.push_back(std::move(o));
+        }
         if (call && throttle) HIP_TRY(hipEventRecord(c->layer_ev[l % jev_ctx::kLayerEvents], s));
     }
 
@@ -812,14 +943,18 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     if (p.n_out == 1) {
         fn.out32 = c->xn.p;
         HIP_TRY(launch_rmsnorm(fn, s));
+        CAP_TRY(cap_add(c, cap, "final_norm", c->xn.p, 1, D));
         GemvArgs g;
         g.K = D;
         g.x = c->xn.p;
         g.nseg = 1;
         g.seg[0] = tab;
         g.y = dout;
-        ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows));
-        HIP_TRY(launch_gemv(g, s));
+        {
+            ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows));
+            HIP_TRY(launch_gemv(g, s));
+        }
+        CAP_TRY(cap_add(c, cap, "logits", dout, 1, tab.rows));
     } else {
         fn.ot = c->xt.p;
         fn.xsum = tab.type == kQ5_1 ? c->xsum.p : nullptr;
@@ -837,6 +972,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         HIP_TRY(launch_gemm(g, s));
     }
     return JEV_OK;
+#undef CAP_TRY
 }
 
 size_t out_floats(const jev_ctx *c, int mode, int n_out, int n_rows)
@@ -974,7 +1110,7 @@ void jev_destroy(jev_ctx *c)
     if (c->vp) (void)hipFree(c->vp);
     c->h.release(); c->y.release(); c->yo.release(); c->ydown.release(); c->q.release();
     c->x32.release(); c->f32.release(); c->xn.release(); c->logits.release();
-    c->part.release(); c->xsum.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->dec_state.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
+    c->part.release(); c->xsum.release(); c->cap32.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->dec_state.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
     if (c->copied) (void)hipEventDestroy(c->copied);
@@ -1183,6 +1319,35 @@ int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *
     // this call: the cache length stays where it was (KvCache.Advance is skipped)
     if (call.cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled");
     c->len = std::max(c->len, p.end); // KvCache.Advance (MinistralModel.cs:360)
+    return JEV_OK;
+}
+
+int jev_capture(jev_ctx *c, const int32_t *tokens, int32_t T, jev_sink sink, void *user, float *logits,
+                size_t out_len)
+{
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (!sink) return fail(JEV_EINVAL, "sink is null");
+    if (!logits || out_len < (size_t)c->cfg.vocab)
+        return fail(JEV_EINVAL, "Expected room for %d logits, got %zu.", c->cfg.vocab, out_len);
+    CallScope call(c);
+    Plan p;
+    rc = prepare(c, tokens, false, T, nullptr, JEV_OUT_LAST_FULL, nullptr, 0, p);
+    if (rc) return rc;
+    HIP_TRY(c->cap32.ensure((size_t)T * std::max(c->cfg.hidden, c->qdim())));
+    HIP_TRY(c->logits.ensure(std::max(c->logits.n, (size_t)c->cfg.vocab)));
+    Capture cap;
+    rc = enqueue_forward(c, p, JEV_OUT_LAST_FULL, 0, c->logits.p, nullptr, &call, false, &cap);
+    if (rc) {
+        (void)hipStreamSynchronize(c->stream);
+        return rc;
+    }
+    HIP_TRY(hipMemcpyAsync(logits, c->logits.p, (size_t)c->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost,
+                           c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (call.cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled");
+    c->len = std::max(c->len, p.end); // KvCache.Advance (MinistralModel.cs:360)
+    for (const Capture::Tap &t : cap.taps) sink(user, t.name.c_str(), t.v.data(), t.rows, t.cols);
     return JEV_OK;
 }
 

@@ -54,6 +54,10 @@ class Layout(ctypes.Structure):
     ]
 
 
+# jev_sink: IActivationSink.Observe (MinistralModel.cs:787-790)
+SINK = ctypes.CFUNCTYPE(None, c_void_p, c_char_p, POINTER(c_float), c_int32, c_int32)
+
+
 class JevError(RuntimeError):
     """A non-zero status from libjev, with the library's message."""
 
@@ -104,6 +108,7 @@ def lib():
         "jev_kv_restore": (c_int, [c_void_p, F32P, c_size_t, c_int32]),
         "jev_forward": (c_int, [c_void_p, I32P, c_int32, POINTER(Layout), c_int, I32P, c_int32, F32P, c_size_t]),
         "jev_forward_tree": (c_int, [c_void_p, I32P, c_int32, I32P, I32P, c_int32, I32P, c_int32, F32P, c_size_t]),
+        "jev_capture": (c_int, [c_void_p, I32P, c_int32, SINK, c_void_p, F32P, c_size_t]),
         "jev_decode_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P]),
         "jev_margins": (c_int, [F32P, c_int32, c_int32, c_int32, c_float, F32P, F32P]),
         "jev_cancel": (None, [c_void_p]),
@@ -148,5 +153,5 @@ EXPORTED = [
     "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
     "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations", "jev_rope_table",
-    "jev_matmul_device_noalloc",
+    "jev_matmul_device_noalloc", "jev_capture",
 ]

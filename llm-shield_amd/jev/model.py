@@ -341,6 +341,22 @@ class MinistralModel:
         L.check(self._lib.jev_decode_greedy(self._h, first, steps, _ptr(out, ctypes.c_int32)))
         return out
 
+    def forward_capture(self, tokens):
+        """ForwardAsync(tokens, capture, options) (MinistralModel.cs:157-160): the last
+        token's logits and every tensor an IActivationSink observes, as
+        [(name, array rows x columns)] in the reference's order."""
+        tok = _i32(tokens)
+        taps = []
+
+        def observe(_user, name, values, rows, cols):
+            taps.append((name.decode(), np.ctypeslib.as_array(values, shape=(rows * cols,)).reshape(rows, cols).copy()))
+
+        sink = L.SINK(observe)
+        out = np.empty(self.config.vocab, np.float32)
+        L.check(self._lib.jev_capture(self._h, _ptr(tok, ctypes.c_int32), len(tok), sink, None,
+                                      _ptr(out, ctypes.c_float), out.size))
+        return out, taps
+
     def cancel(self) -> None:
         self._lib.jev_cancel(self._h)
 

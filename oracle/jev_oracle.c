@@ -16,6 +16,7 @@
 #include "jev_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -637,7 +638,24 @@ struct orc_model {
     /* KvCache (KvCache.cs:12-140): [layer][head][capacity][hd] */
     float **keys, **values;
     int capacity, length;
+    /* the capture of the call in flight (orc_forward_capture), else NULL */
+    orc_sink sink;
+    void *sink_user;
 };
+
+/* capture?.Observe(name, values, rows, columns) */
+static void observe(const orc_model *m, const char *name, const float *v, int rows, int cols)
+{
+    if (m->sink) m->sink(m->sink_user, name, v, rows, cols);
+}
+
+static void observe_layer(const orc_model *m, int l, const char *tap, const float *v, int rows, int cols)
+{
+    char name[64];
+    if (!m->sink) return;
+    snprintf(name, sizeof name, "blk.%d.%s", l, tap);
+    m->sink(m->sink_user, name, v, rows, cols);
+}
 
 static float **kv_alloc(const orc_model *m, int cap)
 {
@@ -792,12 +810,14 @@ int orc_forward(orc_model *m, const int32_t *tokens, int seq, const orc_layout *
 
     for (int t = 0; t < seq; t++) /* QuantMatMul.GatherRows, QuantMatMul.cs:294-305 */
         orc_dequantize(m->embd.type, m->embd.data + (int64_t)tokens[t] * erb, h + (int64_t)t * hidden, hidden);
+    observe(m, "embeddings", h, seq, hidden);
 
     float scale = 1.0f / sqrtf((float)hd);
     int nt = orc_get_threads();
     for (int l = 0; l < c->n_layers; l++) {
         for (int t = 0; t < seq; t++)
             orc_rmsnorm(h + (int64_t)t * hidden, m->attn_norm[l], c->rms_eps, hidden, norm + (int64_t)t * hidden);
+        observe_layer(m, l, "attn_norm", norm, seq, hidden);
         /* AttentionAsync: Q, RotateQueries (:638-647) */
         mm(&m->q[l], norm, seq, q);
         for (int t = 0; t < seq; t++) {
@@ -805,6 +825,7 @@ int orc_forward(orc_model *m, const int32_t *tokens, int seq, const orc_layout *
             orc_rope_apply(m->freqs, m->half, m->mscale, q + (int64_t)t * qdim, heads, hd, p);
             position_scale(m, q + (int64_t)t * qdim, qdim, p);
         }
+        observe_layer(m, l, "q_rope", q, seq, qdim);
         /* K -> StoreKeys (:649-660), V -> StoreValues (:662-669) */
         mm(&m->k[l], norm, seq, kv);
         for (int t = 0; t < seq; t++) {
@@ -813,7 +834,9 @@ int orc_forward(orc_model *m, const int32_t *tokens, int seq, const orc_layout *
             int s = lay ? lay->slot[t] : start + t;
             for (int kh = 0; kh < kvh; kh++) memcpy(kv_row(m->keys, m, l, kh, s), row + kh * hd, sizeof(float) * hd);
         }
+        observe_layer(m, l, "k_rope", kv, seq, kvdim);
         mm(&m->v[l], norm, seq, kv);
+        observe_layer(m, l, "v", kv, seq, kvdim);
         for (int t = 0; t < seq; t++) {
             int s = lay ? lay->slot[t] : start + t;
             for (int kh = 0; kh < kvh; kh++) memcpy(kv_row(m->values, m, l, kh, s), kv + (int64_t)t * kvdim + kh * hd, sizeof(float) * hd);
@@ -838,15 +861,21 @@ int orc_forward(orc_model *m, const int32_t *tokens, int seq, const orc_layout *
             }
             free(scores);
         }
+        observe_layer(m, l, "attn_weighted", ctx, seq, qdim);
         mm(&m->o[l], ctx, seq, scratch);
+        observe_layer(m, l, "attn_out", scratch, seq, hidden);
         for (int i = 0; i < seq * hidden; i++) h[i] = h[i] + scratch[i]; /* Kernels.Add */
+        observe_layer(m, l, "post_attn", h, seq, hidden);
         for (int t = 0; t < seq; t++)
             orc_rmsnorm(h + (int64_t)t * hidden, m->ffn_norm[l], c->rms_eps, hidden, norm + (int64_t)t * hidden);
+        observe_layer(m, l, "ffn_norm", norm, seq, hidden);
         mm(&m->gate[l], norm, seq, g);
         mm(&m->up[l], norm, seq, u);
         orc_swiglu(g, u, g, seq * ff);
         mm(&m->down[l], g, seq, scratch);
+        observe_layer(m, l, "ffn_out", scratch, seq, hidden);
         for (int i = 0; i < seq * hidden; i++) h[i] = h[i] + scratch[i];
+        observe_layer(m, l, "output", h, seq, hidden);
     }
     if (end > m->length) m->length = end; /* KvCache.Advance (:360) */
 
@@ -873,10 +902,23 @@ int orc_forward(orc_model *m, const int32_t *tokens, int seq, const orc_layout *
         free(row);
     } else if (mode == ORC_OUT_LAST_FULL) { /* :411-424 */
         orc_rmsnorm(h + (int64_t)(seq - 1) * hidden, m->out_norm, c->rms_eps, hidden, norm);
+        observe(m, "final_norm", norm, 1, hidden);
         mm(table, norm, 1, out);
+        observe(m, "logits", out, 1, c->vocab);
     }
     free(h); free(norm); free(scratch); free(q); free(ctx); free(kv); free(g); free(u);
     return 0;
+}
+
+int orc_forward_capture(orc_model *m, const int32_t *tokens, int n, orc_sink sink, void *user, float *out,
+                        size_t out_len)
+{
+    m->sink = sink;
+    m->sink_user = user;
+    int rc = orc_forward(m, tokens, n, NULL, ORC_OUT_LAST_FULL, NULL, 0, out, out_len);
+    m->sink = NULL;
+    m->sink_user = NULL;
+    return rc;
 }
 
 int orc_forward_tree(orc_model *m, const int32_t *trunk, int n_trunk, const int32_t *btok,

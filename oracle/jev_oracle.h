@@ -105,6 +105,13 @@ void orc_model_destroy(orc_model *m);
 int orc_model_bind(orc_model *m, int slot, int layer, int type, int rows, int cols, const void *bytes);
 int orc_forward(orc_model *m, const int32_t *tokens, int n, const orc_layout *layout, int mode,
                 const int32_t *rows, int n_rows, float *out, size_t out_len);
+/* IActivationSink.Observe (MinistralModel.cs:787-790). */
+typedef void (*orc_sink)(void *user, const char *name, const float *values, int rows, int columns);
+/* The public ForwardAsync(tokens, capture, options) (MinistralModel.cs:157-160
+ * -> :301-435): causal append with full-vocabulary logits at the last token,
+ * calling `sink` for every tap the reference observes, in its order. */
+int orc_forward_capture(orc_model *m, const int32_t *tokens, int n, orc_sink sink, void *user, float *out,
+                        size_t out_len);
 /* ForwardTreeAsync (MinistralModel.cs:198-219): out = n_branches x n_rows. */
 int orc_forward_tree(orc_model *m, const int32_t *trunk, int n_trunk, const int32_t *branch_tokens,
                      const int32_t *branch_lens, int n_branches, const int32_t *rows, int n_rows,

@@ -41,6 +41,9 @@ class OrcLayout(ctypes.Structure):
 
 _lib = None
 
+# IActivationSink.Observe (MinistralModel.cs:787-790) as a C callback
+SINK = ctypes.CFUNCTYPE(None, c_void_p, ctypes.c_char_p, POINTER(c_float), c_int, c_int)
+
 
 def lib():
     global _lib
@@ -64,6 +67,7 @@ def lib():
             "orc_model_bind": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
             "orc_forward": (c_int, [c_void_p, I, c_int, POINTER(OrcLayout), c_int, I, c_int, F, c_size_t]),
             "orc_forward_tree": (c_int, [c_void_p, I, c_int, I, I, c_int, I, c_int, F, c_size_t]),
+            "orc_forward_capture": (c_int, [c_void_p, I, c_int, SINK, c_void_p, F, c_size_t]),
             "orc_kv_length": (c_int, [c_void_p]),
             "orc_kv_truncate": (None, [c_void_p, c_int]),
             "orc_kv_reset": (None, [c_void_p]),
@@ -331,3 +335,18 @@ class OracleModel:
 
     def forward_branches(self, branches, rows):
         return self.forward_tree([], branches, rows)
+
+    def forward_capture(self, tokens):
+        """ForwardAsync(tokens, capture, options) (MinistralModel.cs:157-160): last-token
+        logits and every observed tap, as [(name, array rows x columns)] in order."""
+        tok = i32(tokens)
+        taps = []
+
+        def observe(_user, name, values, rows, cols):
+            taps.append((name.decode(), np.ctypeslib.as_array(values, shape=(rows * cols,)).reshape(rows, cols).copy()))
+
+        cb = SINK(observe)
+        out = np.empty(self.config.vocab, np.float32)
+        if lib().orc_forward_capture(self._h, ip(tok), len(tok), cb, None, fp(out), out.size) != 0:
+            raise ValueError("oracle forward rejected its arguments")
+        return out, taps

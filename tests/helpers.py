@@ -43,3 +43,17 @@ def tiny_config(**kw):
                 initial_kv_capacity=64)
     base.update(kw)
     return ModelConfig(**base)
+
+
+LAYER_TAPS = ("attn_norm", "q_rope", "k_rope", "v", "attn_weighted", "attn_out", "post_attn", "ffn_norm", "ffn_out",
+              "output")
+
+
+def capture_names(n_layers):
+    """The names ForwardAsync(tokens, capture, options) observes, in order
+    (MinistralModel.cs:331-357 with AttentionAsync's taps at :459, :470, :474,
+    :549, then :418-422)."""
+    names = ["embeddings"]
+    for l in range(n_layers):
+        names += [f"blk.{l}.{t}" for t in LAYER_TAPS]
+    return names + ["final_norm", "logits"]

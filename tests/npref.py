@@ -100,20 +100,30 @@ def rope(x, pos, n_heads, cfg):
     return x.reshape(len(pos), n_heads * hd)
 
 
-def forward(cfg, W, tokens, positions, mask, out_rows):
+def forward(cfg, W, tokens, positions, mask, out_rows, taps=None):
     """tokens [T], positions [T], mask [T, T] (query, key) -> normalised final
-    states at out_rows, and the head logits for them."""
+    states at out_rows, and the head logits for them.  `taps` (a dict) receives
+    the intermediate tensors under the names the reference's activation sink
+    uses (MinistralModel.cs:331-357, :418-422), for a causal call."""
     T = len(tokens)
     hd, H, KV = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     g = H // KV
+    tap = (lambda name, v: taps.__setitem__(name, np.array(v))) if taps is not None else (lambda name, v: None)
     h = W["token_embd.weight"][tokens].copy()
+    tap("embeddings", h)
     for l in range(cfg.n_layers):
         p = f"blk.{l}."
         x = rmsnorm(h, W[p + "attn_norm.weight"], cfg.rms_eps)
+        tap(p + "attn_norm", x)
         q = rope(x @ W[p + "attn_q.weight"].T, positions, H, cfg) * position_scale(cfg, positions)[:, None]
+        tap(p + "q_rope", q)
         q = q.reshape(T, H, hd)
-        k = rope(x @ W[p + "attn_k.weight"].T, positions, KV, cfg).reshape(T, KV, hd)
-        v = (x @ W[p + "attn_v.weight"].T).reshape(T, KV, hd)
+        k = rope(x @ W[p + "attn_k.weight"].T, positions, KV, cfg)
+        tap(p + "k_rope", k)
+        k = k.reshape(T, KV, hd)
+        v = x @ W[p + "attn_v.weight"].T
+        tap(p + "v", v)
+        v = v.reshape(T, KV, hd)
         ctx = np.empty((T, H, hd))
         for head in range(H):
             s = q[:, head, :] @ k[:, head // g, :].T / np.sqrt(hd)
@@ -121,13 +131,24 @@ def forward(cfg, W, tokens, positions, mask, out_rows):
             s = np.exp(s - s.max(-1, keepdims=True))
             s /= s.sum(-1, keepdims=True)
             ctx[:, head, :] = s @ v[:, head // g, :]
-        h = h + ctx.reshape(T, H * hd) @ W[p + "attn_output.weight"].T
+        tap(p + "attn_weighted", ctx.reshape(T, H * hd))
+        a = ctx.reshape(T, H * hd) @ W[p + "attn_output.weight"].T
+        tap(p + "attn_out", a)
+        h = h + a
+        tap(p + "post_attn", h)
         x = rmsnorm(h, W[p + "ffn_norm.weight"], cfg.rms_eps)
+        tap(p + "ffn_norm", x)
         gate = x @ W[p + "ffn_gate.weight"].T
         up = x @ W[p + "ffn_up.weight"].T
-        h = h + (gate / (1 + np.exp(-gate)) * up) @ W[p + "ffn_down.weight"].T
+        f = (gate / (1 + np.exp(-gate)) * up) @ W[p + "ffn_down.weight"].T
+        tap(p + "ffn_out", f)
+        h = h + f
+        tap(p + "output", h)
     hn = rmsnorm(h[out_rows], W["output_norm.weight"], cfg.rms_eps)
-    return hn @ W["token_embd.weight"].T
+    logits = hn @ W["token_embd.weight"].T
+    tap("final_norm", hn[-1:])
+    tap("logits", logits[-1:])
+    return logits
 
 
 def causal_mask(T):

@@ -123,3 +123,27 @@ def test_other_block_types_match_float64_model(t):
     got = oracle.OracleModel(synth.config).bind_synth(synth).forward(tokens)
     ref = npref.forward(synth.config, W, tokens, np.arange(9), npref.causal_mask(9), [8])[0]
     assert worst_close(ref, got) <= 1e-4 and rel_l2(ref, got) <= 1e-5
+
+
+def test_capture_taps_match_float64_model(synth, W):
+    # ForwardAsync(tokens, capture, options): every tap the reference observes
+    # (MinistralModel.cs:331-357, :418-422), in its order and shape, against the
+    # same intermediate of the independent float64 model; and capturing changes
+    # nothing (the logits equal a plain forward bit for bit).
+    from helpers import capture_names
+    cfg = synth.config
+    tokens = jev.random_tokens(21, cfg.vocab, 17)
+    m = open_oracle(synth)
+    m.prefill(tokens[:5])  # a cached prefix: positions and slots start at 5
+    logits, taps = m.forward_capture(tokens[5:])
+    assert [n for n, _ in taps] == capture_names(cfg.n_layers)
+    ref = {}
+    npref.forward(cfg, W, tokens, np.arange(21), npref.causal_mask(21), [20], taps=ref)
+    for name, got in taps:
+        want = ref[name][5:] if ref[name].shape[0] == 21 else ref[name]
+        assert got.shape == want.shape, name
+        assert worst_close(want, got) <= 1e-4, name
+    plain = open_oracle(synth)
+    plain.prefill(tokens[:5])
+    assert np.array_equal(plain.forward(tokens[5:]), logits)
+    assert np.array_equal(taps[-1][1][0], logits)
