@@ -41,6 +41,274 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
+def host_info():
+    """The CPU baseline's host: model name, ISA, and the threads the oracle uses --
+    the host cores visible to this process, capped at 16 (one GPU's share of the
+    host on the GPU boxes this runs on)."""
+    cpus = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    host_isa = "AVX-512" if "avx512f" in flags else ("AVX2" if "avx2" in flags else "x86-64")
+    return {"cpu": model, "cpus_visible": cpus, "threads": max(1, min(16, cpus)),
+            "host_isa": host_isa, "oracle_isa": "x86-64-v3 (AVX2 + FMA; gcc -O3 -march=x86-64-v3)"}
+
+
+def time_best(work, warmups=1, repeats=3, min_sample=0.25, setup=None):
+    """Seconds per call by Benchmark.cs's method (TimeBest / TimeBestAsync, Benchmark.cs:549-623):
+    warm-up calls, then the fastest of `repeats` samples.  Without `setup`, each sample
+    repeats the work until it spans at least `min_sample` seconds (the count fixed by one
+    probe call); with `setup` (run untimed before each sample) every sample is one call."""
+    for _ in range(warmups):
+        if setup:
+            setup()
+        work()
+    if setup is None:
+        t0 = time.perf_counter()
+        work()
+        single = time.perf_counter() - t0
+        inner = 1 if single <= 0 else max(1, min(10_000, int(min_sample / single)))
+    else:
+        inner = 1
+    best = float("inf")
+    for _ in range(max(1, repeats)):
+        if setup:
+            setup()
+        t0 = time.perf_counter()
+        for _ in range(inner):
+            work()
+        best = min(best, (time.perf_counter() - t0) / inner)
+    return best
+
+
+class HipGraph:
+    """A HIP graph captured on one stream (the HIP runtime's C API over ctypes)."""
+
+    def __init__(self, stream, record):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime already loaded by torch / libjev
+        self.stream = ctypes.c_void_p(stream)
+        g, e = ctypes.c_void_p(), ctypes.c_void_p()
+        self._ok(self.hip.hipStreamBeginCapture(self.stream, 1))  # hipStreamCaptureModeThreadLocal
+        try:
+            record()
+        finally:
+            self._ok(self.hip.hipStreamEndCapture(self.stream, ctypes.byref(g)))
+        self.graph = g
+        self._ok(self.hip.hipGraphInstantiate(ctypes.byref(e), g, None, None, ctypes.c_size_t(0)))
+        self.exec = e
+
+    @staticmethod
+    def _ok(rc):
+        if rc != 0:
+            raise RuntimeError(f"HIP graph call failed with status {rc}")
+
+    def launch(self):
+        self._ok(self.hip.hipGraphLaunch(self.exec, self.stream))
+
+    def sync(self):
+        self._ok(self.hip.hipStreamSynchronize(self.stream))
+
+    def close(self):
+        self.hip.hipGraphExecDestroy(self.exec)
+        self.hip.hipGraphDestroy(self.graph)
+
+
+def _oracle(synth, cfg, host):
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    oracle.set_threads(host["threads"])
+    return oracle.OracleModel(cfg).bind_synth(synth)
+
+
+def tree_cpu_baseline(jev, synth, cfg, toks, trunk_n, nb, bl, rows, host):
+    """The 4k-trunk decision takes over a minute of host time on the oracle, so it is
+    sampled: the trunk's first and last 512-token chunks and the 9 x 48 branches are
+    timed, the last chunk and the branches over a cache of the right length (filled
+    through kv_restore; the values do not change the oracle's work).  A chunk's cost
+    grows linearly with the keys before it (its attention), so the 8 trunk chunks
+    sum to 4 * (first + last); the decision is that plus the branches.  One sample
+    of each."""
+    import numpy as np
+    ref = _oracle(synth, cfg, host)
+    branches = [toks[trunk_n + b * bl: trunk_n + (b + 1) * bl] for b in range(nb)]
+    chunk = 512
+    per_pos = 2 * cfg.n_layers * cfg.n_kv_heads * cfg.head_dim
+
+    def timed(prefix, fn):
+        ref.reset_kv_cache()
+        if prefix:
+            ref.kv_restore(np.zeros(per_pos * prefix, np.float32), prefix)
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    t_first = timed(0, lambda: ref.prefill(toks[:chunk]))
+    t_last = timed(trunk_n - chunk, lambda: ref.prefill(toks[trunk_n - chunk:trunk_n]))
+    t_br = timed(trunk_n, lambda: ref.forward_branches(branches, rows))
+    ref.close()
+    n_chunks = trunk_n // chunk
+    est = n_chunks / 2 * (t_first + t_last) + t_br
+    log(f"CPU oracle tree decision: first chunk {t_first:.2f}s, last chunk {t_last:.2f}s, branches {t_br:.2f}s; "
+        f"estimated {est:.1f}s per decision")
+    return {"value": round(est, 2), "unit": "s per decision", "cores": host["threads"], "kind": "port",
+            "extrapolated": True,
+            "sample": f"oracle timed on the trunk's first 512-token chunk ({t_first:.2f} s), its last chunk over 3584 "
+                      f"cached positions ({t_last:.2f} s) and the 9 x 48 branches over 4096 ({t_br:.2f} s), one sample "
+                      f"each; decision = {n_chunks} / 2 * (first + last) + branches (chunk cost linear in the keys "
+                      f"before it)"}
+
+
+def decode_cpu_baseline(jev, synth, cfg, prompt, host):
+    """Q5_1 greedy decode on the oracle after the 512-token prompt: tokens per second
+    over 16 timed steps (one-token passes through the row-dot path and the
+    full-vocabulary head) after 2 warm-up steps."""
+    import numpy as np
+    ref = _oracle(synth, cfg, host)
+    ref.reset_kv_cache()
+    ref.prefill(prompt)
+    nxt = int(prompt[-1])
+    for _ in range(2):
+        nxt = int(np.argmax(ref.forward([nxt])))
+    steps = 16
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        nxt = int(np.argmax(ref.forward([nxt])))
+    dt = (time.perf_counter() - t0) / steps
+    ref.close()
+    log(f"CPU oracle Q5_1 decode: {dt * 1e3:.1f} ms/token ({1 / dt:.2f} tok/s)")
+    return {"value": round(1 / dt, 3), "unit": "tok/s", "cores": host["threads"], "kind": "port",
+            "sample": "16 greedy one-token steps after the 512-token Q5_1 prompt (keys 514..530), 2 warm-up steps, "
+                      "mean over the 16"}
+
+
+def batched_cpu_baseline(jev, synth, cfg, btoks, per, trunk_n, nb, bl, rows, host):
+    """Two of the 64 independent decisions (each 512 + 5 x 32 tokens, identical in
+    shape) on the oracle, each from an empty cache; decisions per second."""
+    ref = _oracle(synth, cfg, host)
+    t0 = time.perf_counter()
+    for d in range(2):
+        t = btoks[d * per:(d + 1) * per]
+        ref.reset_kv_cache()
+        ref.forward_tree(t[:trunk_n], [t[trunk_n + b * bl: trunk_n + (b + 1) * bl] for b in range(nb)], rows)
+    dt = (time.perf_counter() - t0) / 2
+    ref.close()
+    log(f"CPU oracle batched decisions: {dt:.2f}s per decision ({1 / dt:.3f} decisions/s)")
+    return {"value": round(1 / dt, 4), "unit": "decisions/s", "cores": host["threads"], "kind": "port",
+            "extrapolated": True,
+            "sample": "decisions 0 and 1 of the 64 (each 512 + 5 x 32 tokens, verdict rows only) on the oracle, one "
+                      "sample each; the 64 decisions are independent and of the same shape, so the batch rate is "
+                      "the same per decision"}
+
+
+def matmul_leg(args, jev, np, torch, dev, result, host):
+    """Config 1: the repo's single Q8_0 matmul (Benchmark.cs:209-298)."""
+    mr = mc = 3072
+    mt = 256
+    wraw = jev.synth_tensor("bench.matmul.weight", jev.TYPE_Q8_0, mr, mc, 0.02)
+    mx = np.random.default_rng(7).standard_normal((mt, mc)).astype(np.float32)
+    qw = jev.QuantWeight(jev.TYPE_Q8_0, mr, mc, wraw)
+    d_mx = torch.from_numpy(mx).to(dev)
+    d_my = torch.empty((mt, mr), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+    qw.sync()
+    reps = 200
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+    qw.sync()
+    mm_host_s = (time.perf_counter() - t0) / reps
+    mm_flops = 2.0 * mt * mr * mc
+    my = d_my.cpu().numpy()
+    # Benchmark.cs:209-298's single matmul, back to back: 50 calls of the
+    # allocation-free entry point captured in one HIP graph on the weight's
+    # stream, the graph replayed for samples of >= 250 ms, fastest of 3
+    per_graph = 50
+    qw.matmul_device_noalloc(d_mx.data_ptr(), mt, d_my.data_ptr())  # first call: resolves the scratch address
+    qw.sync()
+    graph = HipGraph(qw.stream, lambda: [qw.matmul_device_noalloc(d_mx.data_ptr(), mt, d_my.data_ptr())
+                                         for _ in range(per_graph)])
+
+    def replay():
+        graph.launch()
+        graph.sync()
+
+    mm_s = time_best(replay, warmups=2, repeats=3) / per_graph
+    my_graph = d_my.cpu().numpy()
+    graph.close()
+    graph_bitwise = bool(np.array_equal(my_graph, my))
+    # the opt-in Integer strategy on the same call (activation quantization + int8-MFMA block dots)
+    prev = jev.get_matmul_strategy()
+    jev.set_matmul_strategy(jev.MATMUL_INTEGER)
+    try:
+        for _ in range(5):
+            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+        qw.sync()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
+        qw.sync()
+        mi_s = (time.perf_counter() - t0) / reps
+        my_int = d_my.cpu().numpy()
+    finally:
+        jev.set_matmul_strategy(prev)
+    qw.close()
+    log(f"Q8_0 matmul 256x3072x3072: {mm_s * 1e6:.1f} us/call graph-replayed ({mm_host_s * 1e6:.1f} host-launched), "
+        f"{mm_flops / mm_s / 1e12:.1f} TFLOP/s; integer strategy {mi_s * 1e6:.1f} us/call, "
+        f"{mm_flops / mi_s / 1e12:.1f} TOP/s")
+    result["matmul_q8_0"] = {
+        "workload": "W 3072x3072 N(0,0.02) Q8_0, x 256x3072 N(0,1) fp32 (seed 7), y fp32; "
+                    "split + GEMM + K-split reduce per call; 50 calls per HIP graph, replayed back to back, "
+                    "fastest of 3 samples of >= 250 ms",
+        "us_per_call": round(mm_s * 1e6, 2),
+        "us_per_call_host_launched": round(mm_host_s * 1e6, 2),
+        "graph_result_bitwise_equal": graph_bitwise,
+        "tflops": round(mm_flops / mm_s / 1e12, 2),
+        "mfma_frac": round(mm_flops / mm_s / PEAK_FP16_MFMA, 4),
+        "integer_strategy": {
+            "us_per_call": round(mi_s * 1e6, 2),
+            "tops": round(mm_flops / mi_s / 1e12, 2),
+            "int8_mfma_frac": round(mm_flops / mi_s / PEAK_INT8_MFMA, 4),
+        },
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        from oracle import oracle
+        mm_cpu = {}
+        ref_y = None
+        for thr in (1, host["threads"]):
+            oracle.set_threads(thr)
+
+            def cpu_mm():
+                nonlocal ref_y
+                ref_y = oracle.matmul(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
+
+            mm_cpu[thr] = mm_flops / time_best(cpu_mm, warmups=1, repeats=3) / 1e9
+        err = float(np.max(np.abs(my - ref_y) / np.maximum(1.0, np.abs(ref_y))))
+        result["matmul_q8_0"]["cpu_gflops_by_threads"] = {str(k): round(v, 1) for k, v in mm_cpu.items()}
+        result["matmul_q8_0"]["cpu_baseline"] = {
+            "value": round(mm_cpu[host["threads"]], 1), "unit": "GFLOP/s", "cores": host["threads"],
+            "kind": "port", "sample": "the same 256 x 3072 x 3072 Q8_0 matmul on the oracle's panel path, "
+                                      "fastest of 3 samples of >= 250 ms after a warm-up call"}
+        result["matmul_q8_0"]["parity_worst_rel"] = err
+        t0 = time.perf_counter()
+        ref_int = oracle.matmul_integer(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
+        mi_cpu = mm_flops / (time.perf_counter() - t0) / 1e9
+        result["matmul_q8_0"]["integer_strategy"]["cpu_gops"] = round(mi_cpu, 1)
+        result["matmul_q8_0"]["integer_strategy"]["bitwise_equal_to_oracle"] = bool(
+            np.array_equal(my_int.view(np.uint32), ref_int.view(np.uint32)))
+        log(f"CPU oracle matmul: " + ", ".join(f"{k} threads {v:.1f} GFLOP/s" for k, v in mm_cpu.items())
+            + f"; GPU vs CPU worst {err:.2e}")
+
+
 def prof_read(lib, h, cls):
     n = ctypes.c_int64()
     ms, fl, by = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
@@ -76,6 +344,8 @@ def main():
     ap.add_argument("--gguf-load", action="store_true",
                     help="only write the synthetic Q8_0 checkpoint as a GGUF file in a temporary directory, "
                          "time loading it into HBM through the GGUF reader, and exit")
+    ap.add_argument("--only-matmul", action="store_true",
+                    help="only run the single-matmul leg (config 1) and print its object")
     ap.add_argument("--layers", type=int, default=26, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -122,6 +392,12 @@ def main():
     import jev
     from jev import _lib as L
 
+    host = host_info()
+    if args.only_matmul:
+        res = {}
+        matmul_leg(args, jev, np, torch, torch.device("cuda:0"), res, host)
+        print(json.dumps(res), flush=True)
+        return 0
     cfg = jev.ModelConfig(n_layers=args.layers, initial_kv_capacity=4608)
     t0 = time.time()
     synth = jev.SynthModel(cfg, jev.TYPE_Q8_0)
@@ -290,6 +566,8 @@ def main():
             "attention_tflops": round(ta[2] / (ta[1] * 1e-3) / 1e12, 2) if ta[1] else None,
         }
         result["tree_z"] = [round(float(x), 5) for x in z]
+        if not args.no_cpu:
+            result["tree_cpu_baseline"] = tree_cpu_baseline(jev, synth, cfg, toks, trunk_n, nb, bl, rows, host)
 
     model.close()
 
@@ -339,6 +617,8 @@ def main():
             "decode_attention_ms_per_token": round(da[1] / n_dec, 4),
             "first_tokens": [int(x) for x in toks[:8]],
         }
+        if not args.no_cpu:
+            result["decode_q5_1"]["cpu_baseline"] = decode_cpu_baseline(jev, dsynth, dcfg, prompt, host)
         dmodel.close()
         del dsynth
 
@@ -396,92 +676,31 @@ def main():
             "attention_mfma_frac": round(ba[2] / (ba[1] * 1e-3) / PEAK_FP16_MFMA, 4) if ba[1] else None,
             "z_first": [round(float(x), 4) for x in (zb[0, :, 0] - zb[0, :, 1])],
         }
+        if not args.no_cpu:
+            result["batched_q4_0"]["cpu_baseline"] = batched_cpu_baseline(jev, bsynth, bcfg, btoks, per, trunk_n, nb,
+                                                                          bl, rows, host)
         bmodel.close()
         del bsynth
 
     # ---- single Q8_0 matmul, the repo's bench shape: W 3072 x 3072, x 256 x 3072
     if not args.no_matmul:
-        mr = mc = 3072
-        mt = 256
-        wraw = jev.synth_tensor("bench.matmul.weight", jev.TYPE_Q8_0, mr, mc, 0.02)
-        mx = np.random.default_rng(7).standard_normal((mt, mc)).astype(np.float32)
-        qw = jev.QuantWeight(jev.TYPE_Q8_0, mr, mc, wraw)
-        d_mx = torch.from_numpy(mx).to(dev)
-        d_my = torch.empty((mt, mr), dtype=torch.float32, device=dev)
-        torch.cuda.synchronize()
-        for _ in range(5):
-            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
-        qw.sync()
-        reps = 200
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
-        qw.sync()
-        mm_s = (time.perf_counter() - t0) / reps
-        mm_flops = 2.0 * mt * mr * mc
-        my = d_my.cpu().numpy()
-        # the opt-in Integer strategy on the same call (activation quantization + int8-MFMA block dots)
-        prev = jev.get_matmul_strategy()
-        jev.set_matmul_strategy(jev.MATMUL_INTEGER)
-        try:
-            for _ in range(5):
-                qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
-            qw.sync()
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                qw.matmul_device(d_mx.data_ptr(), mt, d_my.data_ptr())
-            qw.sync()
-            mi_s = (time.perf_counter() - t0) / reps
-            my_int = d_my.cpu().numpy()
-        finally:
-            jev.set_matmul_strategy(prev)
-        qw.close()
-        log(f"Q8_0 matmul 256x3072x3072: {mm_s * 1e6:.1f} us/call, {mm_flops / mm_s / 1e12:.1f} TFLOP/s; "
-            f"integer strategy {mi_s * 1e6:.1f} us/call, {mm_flops / mi_s / 1e12:.1f} TOP/s")
-        result["matmul_q8_0"] = {
-            "workload": "W 3072x3072 N(0,0.02) Q8_0, x 256x3072 N(0,1) fp32 (seed 7), y fp32; "
-                        "split + GEMM (+ K-split reduce) per call, back to back",
-            "us_per_call": round(mm_s * 1e6, 2),
-            "tflops": round(mm_flops / mm_s / 1e12, 2),
-            "mfma_frac": round(mm_flops / mm_s / PEAK_FP16_MFMA, 4),
-            "integer_strategy": {
-                "us_per_call": round(mi_s * 1e6, 2),
-                "tops": round(mm_flops / mi_s / 1e12, 2),
-                "int8_mfma_frac": round(mm_flops / mi_s / PEAK_INT8_MFMA, 4),
-            },
-        }
-        if not args.no_cpu:
-            sys.path.insert(0, ROOT)
-            from oracle import oracle
-            mm_cpu = {}
-            for thr in (1, max(1, min(16, os.cpu_count() or 1))):
-                oracle.set_threads(thr)
-                t0 = time.perf_counter()
-                ref_y = oracle.matmul(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
-                mm_cpu[thr] = mm_flops / (time.perf_counter() - t0) / 1e9
-            err = float(np.max(np.abs(my - ref_y) / np.maximum(1.0, np.abs(ref_y))))
-            result["matmul_q8_0"]["cpu_gflops_by_threads"] = {str(k): round(v, 1) for k, v in mm_cpu.items()}
-            result["matmul_q8_0"]["parity_worst_rel"] = err
-            t0 = time.perf_counter()
-            ref_int = oracle.matmul_integer(jev.TYPE_Q8_0, wraw, mr, mc, mx, mt)
-            mi_cpu = mm_flops / (time.perf_counter() - t0) / 1e9
-            result["matmul_q8_0"]["integer_strategy"]["cpu_gops"] = round(mi_cpu, 1)
-            result["matmul_q8_0"]["integer_strategy"]["bitwise_equal_to_oracle"] = bool(
-                np.array_equal(my_int.view(np.uint32), ref_int.view(np.uint32)))
-            log(f"CPU oracle matmul: " + ", ".join(f"{k} threads {v:.1f} GFLOP/s" for k, v in mm_cpu.items())
-                + f"; GPU vs CPU worst {err:.2e}")
+        matmul_leg(args, jev, np, torch, dev, result, host)
 
     # ---- CPU baseline: the oracle on the host cores, one 256-token prefill
     if not args.no_cpu:
         sys.path.insert(0, ROOT)
         from oracle import oracle
 
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host["threads"]
         oracle.set_threads(threads)
         ref = oracle.OracleModel(cfg).bind_synth(synth)
-        t0 = time.perf_counter()
-        cpu_logits = ref.forward(tokens)
-        cpu_s = time.perf_counter() - t0
+        cpu_logits = None
+
+        def cpu_prefill():
+            nonlocal cpu_logits
+            cpu_logits = ref.forward(tokens)
+
+        cpu_s = time_best(cpu_prefill, warmups=1, repeats=3, setup=ref.reset_kv_cache)
         err = float(np.max(np.abs(gpu_logits - cpu_logits) / np.maximum(1.0, np.abs(cpu_logits))))
         log(f"CPU oracle: {cpu_s:.2f}s for the 256-token prefill ({threads} threads); GPU vs CPU logits worst {err:.2e}")
         result["cpu_baseline"] = {
@@ -489,8 +708,10 @@ def main():
             "unit": "tok/s",
             "cores": threads,
             "kind": "port",
-            "sample": "one full 256-token Q8_0 prefill + final-position full-vocab logits of the same 26-layer "
-                      "synthetic model (C restatement of the reference's managed Float path)",
+            "sample": "the full 256-token Q8_0 prefill + final-position full-vocab logits of the same 26-layer "
+                      "synthetic model on the oracle (C restatement of the reference's managed Float path), "
+                      "fastest of 3 after a warm-up",
+            "host": host,
         }
         result["parity_logits_worst_rel"] = err
         ref.close()

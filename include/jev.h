@@ -229,6 +229,10 @@ int jev_matmul_device(jev_weight *w, const float *x, int32_t tokens, float *y);
  * (on different weights' streams, or from several threads) race. */
 int jev_matmul_device_noalloc(jev_weight *w, const float *x, int32_t tokens, float *y);
 int jev_weight_sync(jev_weight *w);
+/* The weight's HIP stream (hipStream_t): the caller may capture calls on it
+ * into a HIP graph (jev_matmul_device_noalloc allocates nothing, so it can be
+ * captured) or time them with events. */
+void *jev_weight_stream(jev_weight *w);
 
 /* QuantMatMul.Strategy (QuantMatMul.cs:10-41), process-wide, read by every
  * jev_matmul_device / jev_matmul_q call.  AUTO and FLOAT take the float path

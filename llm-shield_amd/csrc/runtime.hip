@@ -1918,6 +1918,8 @@ int jev_matmul_device_noalloc(jev_weight *h, const float *x, int32_t tokens, flo
     return JEV_OK;
 }
 
+void *jev_weight_stream(jev_weight *h) { return h ? (void *)h->stream : nullptr; }
+
 int jev_weight_sync(jev_weight *h)
 {
     if (!h) return fail(JEV_EINVAL, "null weight");

@@ -123,6 +123,7 @@ def lib():
         "jev_matmul_device": (c_int, [c_void_p, c_void_p, c_int32, c_void_p]),
         "jev_matmul_device_noalloc": (c_int, [c_void_p, c_void_p, c_int32, c_void_p]),
         "jev_weight_sync": (c_int, [c_void_p]),
+        "jev_weight_stream": (c_void_p, [c_void_p]),
         "jev_rope_table": (c_int, [POINTER(Config), F32P, c_int32, F32P]),
         "jev_dequantize": (c_int, [c_int, c_void_p, c_size_t, F32P, c_int64]),
         "jev_matmul_q": (c_int, [c_int, c_void_p, c_int64, c_int64, F32P, c_int32, F32P]),
@@ -153,5 +154,5 @@ EXPORTED = [
     "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
     "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations", "jev_rope_table",
-    "jev_matmul_device_noalloc", "jev_capture",
+    "jev_matmul_device_noalloc", "jev_capture", "jev_weight_stream",
 ]

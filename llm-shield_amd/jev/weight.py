@@ -43,6 +43,11 @@ class QuantWeight:
     def sync(self) -> None:
         L.check(self._lib.jev_weight_sync(self._h))
 
+    @property
+    def stream(self) -> int:
+        """The weight's HIP stream handle (for graph capture or event timing by the caller)."""
+        return int(self._lib.jev_weight_stream(self._h) or 0)
+
 
 def set_matmul_strategy(strategy: int) -> None:
     """QuantMatMul.Strategy setter (QuantMatMul.cs:41): process-wide, read by
