@@ -566,6 +566,29 @@ def main():
             "attention_tflops": round(ta[2] / (ta[1] * 1e-3) / 1e12, 2) if ta[1] else None,
         }
         result["tree_z"] = [round(float(x), 5) for x in z]
+        # N1: the trunk's KV state (4096 positions, 872 MB) snapshotted and restored
+        # inside HBM (the decider's question snapshot), against the host copy
+        L.check(lib.jev_sync(h))
+        snaps = []
+
+        def drop_snaps():
+            for x in snaps:
+                x.close()
+            snaps.clear()
+
+        t_snap = time_best(lambda: snaps.append(model.kv_snapshot_device(trunk_n)), warmups=1, repeats=3,
+                           setup=drop_snaps)
+        snap = snaps[-1]
+        t_restore = time_best(lambda: model.kv_restore(snap), warmups=1, repeats=3)
+        t_host = time_best(lambda: model.kv_snapshot(trunk_n), warmups=0, repeats=2, setup=lambda: None)
+        for x in snaps:
+            x.close()
+        kv_bytes = 2 * cfg.n_layers * cfg.n_kv_heads * trunk_n * cfg.head_dim * 4
+        log(f"KV snapshot of {trunk_n} positions ({kv_bytes / 1e6:.0f} MB): device {t_snap * 1e3:.2f} ms, restore "
+            f"{t_restore * 1e3:.2f} ms; to host {t_host * 1e3:.1f} ms")
+        result["kv_snapshot_4096"] = {"bytes": kv_bytes, "device_snapshot_ms": round(t_snap * 1e3, 3),
+                                      "device_restore_ms": round(t_restore * 1e3, 3),
+                                      "host_snapshot_ms": round(t_host * 1e3, 2)}
         if not args.no_cpu:
             result["tree_cpu_baseline"] = tree_cpu_baseline(jev, synth, cfg, toks, trunk_n, nb, bl, rows, host)
 

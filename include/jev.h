@@ -128,6 +128,20 @@ int jev_kv_reset(jev_ctx *ctx);                                  /* Reset :43   
 int jev_kv_snapshot(jev_ctx *ctx, int32_t length, float *out, size_t n_floats); /* Snapshot :94-112 */
 int jev_kv_restore(jev_ctx *ctx, const float *in, size_t n_floats, int32_t length); /* Restore :115-136 */
 
+/* The same snapshot kept in HBM (KvCache.Snapshot/Restore, KvCache.cs:94-136, as
+ * JevstralDecider's question-snapshot LRU and the system-prompt snapshot use it,
+ * JevstralDecider.cs:259-266, :348-354): taking and restoring one is a copy
+ * inside device memory, never through the host.  The handle owns its HBM
+ * (2 x layers x kv heads x length x head_dim floats) until destroyed; it can
+ * be restored into any context of the same geometry on the same device.
+ * jev_snapshot_read copies it out in jev_kv_snapshot's flat layout (SHKV files). */
+typedef struct jev_snapshot jev_snapshot;
+int jev_kv_snapshot_device(jev_ctx *ctx, int32_t length, jev_snapshot **out);
+int jev_kv_restore_device(jev_ctx *ctx, const jev_snapshot *snapshot);
+int jev_snapshot_length(const jev_snapshot *snapshot, int32_t *length);
+int jev_snapshot_read(const jev_snapshot *snapshot, float *out, size_t n_floats);
+void jev_snapshot_destroy(jev_snapshot *snapshot);
+
 /* The private ForwardAsync (MinistralModel.cs:301-435).  layout NULL = plain
  * causal append after the cached tokens.  out receives (by mode): nothing;
  * vocab floats; n_outputs * n_rows floats; n_outputs * vocab floats, where

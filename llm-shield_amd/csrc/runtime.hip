@@ -1244,6 +1244,25 @@ int jev_kv_reset(jev_ctx *c)
     return JEV_OK;
 }
 
+// Copies positions [0, length) of every [layer][kv head] of the cache's K and V
+// between the arena (rows `cap` positions apart) and a flat buffer in
+// KvCache.Snapshot's order (KvCache.cs:94-112): keys [l][h][0..length)[hd],
+// then values.  One pitched copy per array.
+static int kv_flat_copy(jev_ctx *c, int32_t length, float *flat, bool to_flat, hipMemcpyKind kind)
+{
+    const jev_config &f = c->cfg;
+    const size_t heads = (size_t)f.n_layers * f.n_kv_heads, row = (size_t)length * f.head_dim * sizeof(float);
+    const size_t pitch = (size_t)c->cap * f.head_dim * sizeof(float);
+    if (length == 0) return JEV_OK;
+    for (int pass = 0; pass < 2; pass++) {
+        float *arena = pass ? c->vc : c->kc;
+        float *dense = flat + (size_t)pass * heads * length * f.head_dim;
+        if (to_flat) HIP_TRY(hipMemcpy2DAsync(dense, row, arena, pitch, row, heads, kind, c->stream));
+        else HIP_TRY(hipMemcpy2DAsync(arena, pitch, dense, row, row, heads, kind, c->stream));
+    }
+    return JEV_OK;
+}
+
 // KvCache.Snapshot (KvCache.cs:94-112): keys of every [layer][head], then values.
 int jev_kv_snapshot(jev_ctx *c, int32_t length, float *out, size_t n)
 {
@@ -1253,15 +1272,23 @@ int jev_kv_snapshot(jev_ctx *c, int32_t length, float *out, size_t n)
     size_t per = (size_t)f.n_layers * f.n_kv_heads * length * f.head_dim;
     if (n != per * 2) return fail(JEV_EINVAL, "Snapshot needs %zu floats; got %zu.", per * 2, n);
     HIP_TRY(hipSetDevice(c->device));
-    size_t cur = 0, row = (size_t)length * f.head_dim;
-    for (int pass = 0; pass < 2; pass++)
-        for (int l = 0; l < f.n_layers; l++)
-            for (int h = 0; h < f.n_kv_heads; h++) {
-                const float *src = (pass ? c->vc : c->kc) + (size_t)l * c->layer_stride() + (size_t)h * c->cap * f.head_dim;
-                HIP_TRY(hipMemcpyAsync(out + cur, src, row * sizeof(float), hipMemcpyDeviceToHost, c->stream));
-                cur += row;
-            }
+    int rc = kv_flat_copy(c, length, out, true, hipMemcpyDeviceToHost);
+    if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
+    return JEV_OK;
+}
+
+// Leaves the cache holding exactly `length` positions from a flat K / V
+// buffer already in the arena (KvCache.Restore's end state): the fp16-pair
+// shadows the prefill attention reads are rebuilt from the fp32 rows.
+static int kv_finish_restore(jev_ctx *c, int32_t length)
+{
+    const jev_config &f = c->cfg;
+    const int heads = f.n_layers * f.n_kv_heads;
+    HIP_TRY(launch_kv_split(c->kc, c->kp, heads, c->cap, length, f.head_dim, c->stream));
+    HIP_TRY(launch_kv_split(c->vc, c->vp, heads, c->cap, length, f.head_dim, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->len = length;
     return JEV_OK;
 }
 
@@ -1276,20 +1303,87 @@ int jev_kv_restore(jev_ctx *c, const float *in, size_t n, int32_t length)
     HIP_TRY(hipSetDevice(c->device));
     int rc = kv_ensure(c, length);
     if (rc) return rc;
-    size_t cur = 0, row = (size_t)length * f.head_dim;
-    for (int pass = 0; pass < 2; pass++)
-        for (int l = 0; l < f.n_layers; l++)
-            for (int h = 0; h < f.n_kv_heads; h++) {
-                float *dst = (pass ? c->vc : c->kc) + (size_t)l * c->layer_stride() + (size_t)h * c->cap * f.head_dim;
-                HIP_TRY(hipMemcpyAsync(dst, in + cur, row * sizeof(float), hipMemcpyHostToDevice, c->stream));
-                cur += row;
-            }
-    const int heads = f.n_layers * f.n_kv_heads;
-    HIP_TRY(launch_kv_split(c->kc, c->kp, heads, c->cap, length, f.head_dim, c->stream));
-    HIP_TRY(launch_kv_split(c->vc, c->vp, heads, c->cap, length, f.head_dim, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
-    c->len = length;
+    rc = kv_flat_copy(c, length, const_cast<float *>(in), false, hipMemcpyHostToDevice);
+    if (rc) return rc;
+    return kv_finish_restore(c, length);
+}
+
+// A snapshot kept in HBM: the same flat layout as jev_kv_snapshot's output.
+struct jev_snapshot {
+    int device = 0;
+    int32_t layers = 0, kv_heads = 0, head_dim = 0, length = 0;
+    float *data = nullptr; // keys then values, KvCache.Snapshot order
+    size_t floats = 0;
+};
+
+int jev_kv_snapshot_device(jev_ctx *c, int32_t length, jev_snapshot **out)
+{
+    if (!c || !out) return fail(JEV_EINVAL, "null argument");
+    *out = nullptr;
+    if (length < 0 || length > c->len) return fail(JEV_EINVAL, "Only %d positions are cached.", c->len);
+    const jev_config &f = c->cfg;
+    HIP_TRY(hipSetDevice(c->device));
+    jev_snapshot *sn = new jev_snapshot;
+    sn->device = c->device;
+    sn->layers = f.n_layers;
+    sn->kv_heads = f.n_kv_heads;
+    sn->head_dim = f.head_dim;
+    sn->length = length;
+    sn->floats = 2 * (size_t)f.n_layers * f.n_kv_heads * length * f.head_dim;
+    hipError_t e = hipMalloc((void **)&sn->data, std::max<size_t>(sn->floats, 1) * sizeof(float));
+    if (e != hipSuccess) {
+        delete sn;
+        return fail(JEV_ENOMEM, "device snapshot of %d positions (%zu bytes): %s", length, sn->floats * 4,
+                    hipGetErrorString(e));
+    }
+    int rc = kv_flat_copy(c, length, sn->data, true, hipMemcpyDeviceToDevice);
+    if (!rc && (e = hipStreamSynchronize(c->stream)) != hipSuccess) rc = fail(JEV_EDEVICE, "snapshot: %s", hipGetErrorString(e));
+    if (rc) {
+        jev_snapshot_destroy(sn);
+        return rc;
+    }
+    *out = sn;
     return JEV_OK;
+}
+
+int jev_kv_restore_device(jev_ctx *c, const jev_snapshot *sn)
+{
+    if (!c || !sn) return fail(JEV_EINVAL, "null argument");
+    const jev_config &f = c->cfg;
+    if (sn->layers != f.n_layers || sn->kv_heads != f.n_kv_heads || sn->head_dim != f.head_dim)
+        return fail(JEV_EINVAL, "The snapshot was taken for %d layers x %d KV heads x %d; this model has %d x %d x %d.",
+                    sn->layers, sn->kv_heads, sn->head_dim, f.n_layers, f.n_kv_heads, f.head_dim);
+    if (sn->device != c->device) return fail(JEV_EINVAL, "the snapshot lives on device %d, the model on %d", sn->device, c->device);
+    HIP_TRY(hipSetDevice(c->device));
+    int rc = kv_ensure(c, sn->length);
+    if (rc) return rc;
+    rc = kv_flat_copy(c, sn->length, sn->data, false, hipMemcpyDeviceToDevice);
+    if (rc) return rc;
+    return kv_finish_restore(c, sn->length);
+}
+
+int jev_snapshot_length(const jev_snapshot *sn, int32_t *length)
+{
+    if (!sn || !length) return fail(JEV_EINVAL, "null argument");
+    *length = sn->length;
+    return JEV_OK;
+}
+
+int jev_snapshot_read(const jev_snapshot *sn, float *out, size_t n)
+{
+    if (!sn || !out) return fail(JEV_EINVAL, "null argument");
+    if (n != sn->floats) return fail(JEV_EINVAL, "Snapshot needs %zu floats; got %zu.", sn->floats, n);
+    HIP_TRY(hipSetDevice(sn->device));
+    if (n) HIP_TRY(hipMemcpy(out, sn->data, n * sizeof(float), hipMemcpyDeviceToHost));
+    return JEV_OK;
+}
+
+void jev_snapshot_destroy(jev_snapshot *sn)
+{
+    if (!sn) return;
+    (void)hipSetDevice(sn->device);
+    if (sn->data) (void)hipFree(sn->data);
+    delete sn;
 }
 
 int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *layout, int mode,

@@ -106,6 +106,11 @@ def lib():
         "jev_kv_reset": (c_int, [c_void_p]),
         "jev_kv_snapshot": (c_int, [c_void_p, c_int32, F32P, c_size_t]),
         "jev_kv_restore": (c_int, [c_void_p, F32P, c_size_t, c_int32]),
+        "jev_kv_snapshot_device": (c_int, [c_void_p, c_int32, POINTER(c_void_p)]),
+        "jev_kv_restore_device": (c_int, [c_void_p, c_void_p]),
+        "jev_snapshot_length": (c_int, [c_void_p, I32P]),
+        "jev_snapshot_read": (c_int, [c_void_p, F32P, c_size_t]),
+        "jev_snapshot_destroy": (None, [c_void_p]),
         "jev_forward": (c_int, [c_void_p, I32P, c_int32, POINTER(Layout), c_int, I32P, c_int32, F32P, c_size_t]),
         "jev_forward_tree": (c_int, [c_void_p, I32P, c_int32, I32P, I32P, c_int32, I32P, c_int32, F32P, c_size_t]),
         "jev_capture": (c_int, [c_void_p, I32P, c_int32, SINK, c_void_p, F32P, c_size_t]),
@@ -154,5 +159,6 @@ EXPORTED = [
     "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
     "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations", "jev_rope_table",
-    "jev_matmul_device_noalloc", "jev_capture", "jev_weight_stream",
+    "jev_matmul_device_noalloc", "jev_capture", "jev_weight_stream", "jev_kv_snapshot_device",
+    "jev_kv_restore_device", "jev_snapshot_length", "jev_snapshot_read", "jev_snapshot_destroy",
 ]

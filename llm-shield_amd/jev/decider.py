@@ -69,7 +69,7 @@ class DecisionResult:
 @dataclass
 class _QuestionSnapshot:
     tokens: np.ndarray
-    state: np.ndarray
+    state: object  # a DeviceSnapshot (HBM) when the model offers one, else the flat host array
 
 
 class TreeDecider:
@@ -118,7 +118,7 @@ class TreeDecider:
         question_length = common_prefix(prefix, question_tokens)
         snapshot = self._find_snapshot(prefix, start) if start < question_length else None
         if snapshot is not None:
-            m.kv_restore(snapshot.state, len(snapshot.tokens))
+            m.kv_restore(snapshot.state, len(snapshot.tokens))  # a copy inside HBM for a device snapshot
             start = len(snapshot.tokens)
             self._question_hits += 1
         elif start > 0 and start >= self.system_tokens:
@@ -167,7 +167,9 @@ class TreeDecider:
         for q in self._questions:
             if len(q.tokens) == question_length and common_prefix(prefix, q.tokens) == question_length:
                 return
-        self._questions.append(_QuestionSnapshot(prefix[:question_length].copy(),
-                                                 self.model.kv_snapshot(question_length)))
+        take = getattr(self.model, "kv_snapshot_device", None) or self.model.kv_snapshot
+        self._questions.append(_QuestionSnapshot(prefix[:question_length].copy(), take(question_length)))
         while len(self._questions) > self.question_cache_size:
-            self._questions.pop(0)
+            evicted = self._questions.pop(0)
+            if hasattr(evicted.state, "close"):
+                evicted.state.close()

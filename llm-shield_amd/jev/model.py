@@ -170,6 +170,36 @@ class TokenLayout:
         return c
 
 
+class DeviceSnapshot:
+    """A KV snapshot resident in HBM (jev_kv_snapshot_device); restore it with
+    MinistralModel.kv_restore, read it out with to_host (KvCache.Snapshot's
+    flat layout, what SHKV files hold)."""
+
+    def __init__(self, handle: ctypes.c_void_p, config: ModelConfig):
+        self.handle = handle
+        self._lib = L.lib()
+        n = ctypes.c_int32()
+        L.check(self._lib.jev_snapshot_length(handle, ctypes.byref(n)))
+        self.length = int(n.value)
+        self.floats = 2 * config.n_layers * config.n_kv_heads * self.length * config.head_dim
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.floats, np.float32)
+        L.check(self._lib.jev_snapshot_read(self.handle, _ptr(out, ctypes.c_float), out.size))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) and self.handle.value:
+            self._lib.jev_snapshot_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class MinistralModel:
     """One libjev context: device weights, the HBM KV cache and a stream.
 
@@ -247,9 +277,22 @@ class MinistralModel:
         L.check(self._lib.jev_kv_snapshot(self._h, length, _ptr(out, ctypes.c_float), n))
         return out
 
-    def kv_restore(self, snapshot: np.ndarray, length: int) -> None:
+    def kv_restore(self, snapshot, length: Optional[int] = None) -> None:
+        """KvCache.Restore (KvCache.cs:115-136) from a flat host array (length
+        positions) or from a DeviceSnapshot (its own length)."""
+        if isinstance(snapshot, DeviceSnapshot):
+            if length is not None and length != snapshot.length:
+                raise L.ArgumentError(L.JEV_EINVAL, f"the snapshot holds {snapshot.length} positions, not {length}")
+            L.check(self._lib.jev_kv_restore_device(self._h, snapshot.handle))
+            return
         s = np.ascontiguousarray(snapshot, dtype=np.float32)
         L.check(self._lib.jev_kv_restore(self._h, _ptr(s, ctypes.c_float), s.size, length))
+
+    def kv_snapshot_device(self, length: int) -> "DeviceSnapshot":
+        """KvCache.Snapshot kept in HBM: a copy inside device memory."""
+        h = ctypes.c_void_p()
+        L.check(self._lib.jev_kv_snapshot_device(self._h, length, ctypes.byref(h)))
+        return DeviceSnapshot(h, self.config)
 
     # ------------------------------------------------------------ forward
     def forward_layout(self, tokens, layout: Optional[TokenLayout], mode: int, rows=None) -> np.ndarray:

@@ -100,10 +100,14 @@ def fingerprint(model, tokens: Sequence[int]) -> str:
 class SystemPromptCache:
     """A captured prefix: its tokens, the flat KV state and the fingerprint."""
 
-    def __init__(self, tokens: Sequence[int], state: np.ndarray, fingerprint_hex: str):
+    def __init__(self, tokens: Sequence[int], state: np.ndarray, fingerprint_hex: str, device=None):
         self.tokens = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).ravel())
         self.state = np.ascontiguousarray(np.asarray(state, dtype=np.float32).ravel())
         self.fingerprint = fingerprint_hex
+        # the same state kept in HBM (a DeviceSnapshot of the model it was
+        # captured or first restored into): later restores copy inside device memory
+        self._device = device
+        self._device_model = None
 
     @property
     def token_count(self) -> int:
@@ -120,7 +124,12 @@ class SystemPromptCache:
         toks = np.asarray(tokens, dtype=np.int32).ravel()
         model.reset_kv_cache()
         model.prefill(toks)
-        return cls(toks, model.kv_snapshot(len(toks)), fingerprint(model, toks))
+        take_device = getattr(model, "kv_snapshot_device", None)
+        device = take_device(len(toks)) if take_device else None
+        host = device.to_host() if device is not None else model.kv_snapshot(len(toks))
+        cache = cls(toks, host, fingerprint(model, toks), device)
+        cache._device_model = model if device is not None else None
+        return cache
 
     def restore_into(self, model) -> None:
         """RestoreInto (SystemPromptCache.cs:67-75): refuses a snapshot taken
@@ -130,7 +139,15 @@ class SystemPromptCache:
             raise InvalidOperationError(
                 f"This snapshot was captured for a different model or prefix "
                 f"(fingerprint {self.fingerprint}, model reports {expected}).")
+        if self._device is not None and self._device_model is model:
+            model.kv_restore(self._device)
+            return
         model.kv_restore(self.state, self.token_count)
+        take_device = getattr(model, "kv_snapshot_device", None)
+        if take_device is not None:
+            if self._device is not None:
+                self._device.close()
+            self._device, self._device_model = take_device(self.token_count), model
 
     def is_prefix_of(self, tokens: Sequence[int]) -> bool:
         """IsPrefixOf (SystemPromptCache.cs:81-82)."""

@@ -112,3 +112,40 @@ def test_interleaved_questions_are_restored_from_their_snapshots(model):
     assert warm.question_cache_hits == 1
     assert restored.cached_tokens == len(q) > cold.cached_tokens
     assert np.array_equal(restored.margins, cold.margins)
+
+
+def test_device_snapshot_matches_the_host_snapshot_and_restores_bitwise(gpu, synth, model):
+    """The HBM snapshot (jev_kv_snapshot_device) holds exactly KvCache.Snapshot's flat state, and a
+    restore from it (a copy inside device memory, pair shadows rebuilt) continues bit for bit like
+    the whole prompt -- also after the cache grew, and into a second context of the same model."""
+    tokens = _tok(150, 31)
+    model.reset_kv_cache()
+    whole = model.forward(tokens)
+    model.reset_kv_cache()
+    model.prefill(tokens[:90])  # initial capacity 64: the arena grew to 128
+    snap = model.kv_snapshot_device(90)
+    assert snap.length == 90 and np.array_equal(snap.to_host(), model.kv_snapshot(90))
+    model.reset_kv_cache()
+    model.forward(_tok(200, 32))  # overwrite the arena and grow it again
+    model.kv_restore(snap)
+    assert model.cached_token_count == 90
+    assert np.array_equal(model.forward(tokens[90:]), whole)
+    with synth.open(0) as other:
+        other.kv_restore(snap)
+        assert np.array_equal(other.forward(tokens[90:]), whole)
+    snap.close()
+
+
+def test_device_snapshot_refuses_another_geometry(gpu, model):
+    model.reset_kv_cache()
+    model.prefill(_tok(20, 33))
+    snap = model.kv_snapshot_device(20)
+    other = jev.SynthModel(tiny_config(n_kv_heads=1, n_heads=2), jev.TYPE_Q8_0).open(0)
+    try:
+        with pytest.raises(jev.ArgumentError, match="KV heads"):
+            other.kv_restore(snap)
+        with pytest.raises(jev.ArgumentError):
+            model.kv_snapshot_device(21)  # more than cached
+    finally:
+        other.close()
+        snap.close()
