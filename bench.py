@@ -8,7 +8,9 @@ second with the token ids and the model already resident in HBM.  Beside it:
   * the 4096-token-trunk, 9 x 48-token-branch tree decision (Q8_0, verdict
     rows only) in ms per decision;
   * the Q5_1 decode loop: 512-token prefill, then 128 greedy steps, ms per
-    token and the decode GEMVs' achieved HBM bandwidth;
+    token and the decode GEMVs' achieved HBM bandwidth; and on the same model
+    the reasoning decider's rows decode (12 rows x 256-token prompts, 32
+    steps of one token per row) as a replayed graph beside the host loop;
   * 64 independent Q4_0 decisions (512-token trunk + 5 x 32-token branches
     each) evaluated in one tree-masked pass, decisions per second;
   * the repo's single Q8_0 matmul (3072 x 3072 weight, 256 tokens), TFLOP/s,
@@ -315,6 +317,59 @@ def prof_read(lib, h, cls):
     rc = lib.jev_profile_read(h, cls, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by))
     assert rc == 0
     return n.value, ms.value, fl.value, by.value
+
+
+def rows_decode_leg(jev, np, L, lib, model, n_rows=12, plen=256, steps=32):
+    """ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178):
+    n_rows rows of one cache, each prompt prefilled alone, then one token per
+    row per step.  Timed two ways from the same state: the replayed device
+    graph (jev_decode_rows_greedy) and the reference's host loop, one
+    ForwardRowsAsync-style jev_forward per step with full-vocabulary logits
+    copied back and the argmax taken on the host.  Both must give the same
+    tokens (two or more rows: batch-invariant kernels)."""
+    h = model.handle
+    prompts = [jev.random_tokens(plen, model.config.vocab, 50 + r) for r in range(n_rows)]
+    bases = jev.row_bases([plen] * n_rows, steps + 1)
+
+    def start():
+        L.check(lib.jev_kv_reset(h))
+        first = [jev.index_of_max(model.forward_rows(0, [bases[r]], [0], [list(prompts[r])])[0])
+                 for r in range(n_rows)]
+        L.check(lib.jev_sync(h))
+        return first
+
+    def graph_run():
+        first = start()
+        t = time.perf_counter()
+        out = model.decode_rows_greedy(0, bases, [plen] * n_rows, first, steps)
+        return time.perf_counter() - t, out
+
+    def host_run():
+        first = start()
+        lengths, nxt, outs = [plen] * n_rows, first, []
+        t = time.perf_counter()
+        for _ in range(steps):
+            z = model.forward_rows(0, bases, lengths, [[x] for x in nxt])
+            lengths = [n + 1 for n in lengths]
+            nxt = [jev.index_of_max(v) for v in z]
+            outs.append(nxt)
+        return time.perf_counter() - t, np.array(outs, np.int32)
+
+    graph_run()
+    tg, og = min((graph_run() for _ in range(2)), key=lambda r: r[0])
+    th, oh = min((host_run() for _ in range(2)), key=lambda r: r[0])
+    same = bool(np.array_equal(og, oh))
+    log(f"rows decode ({n_rows} rows x {plen}-token prompts, {steps} steps): graph {tg / steps * 1e3:.3f} ms/step, "
+        f"host loop {th / steps * 1e3:.3f} ms/step, tokens equal: {same}")
+    return {
+        "workload": f"{n_rows} rows, each a {plen}-token prompt prefilled alone, then {steps} greedy steps of one "
+                    "token per row (full-vocabulary logits per row, argmax)",
+        "graph_ms_per_step": round(tg / steps * 1e3, 4),
+        "graph_tok_s": round(n_rows * steps / tg, 1),
+        "host_loop_ms_per_step": round(th / steps * 1e3, 4),
+        "host_loop_tok_s": round(n_rows * steps / th, 1),
+        "tokens_equal": same,
+    }
 
 
 def batched_decisions_layout(nd, trunk_n, nb, bl):
@@ -642,6 +697,8 @@ def main():
         }
         if not args.no_cpu:
             result["decode_q5_1"]["cpu_baseline"] = decode_cpu_baseline(jev, dsynth, dcfg, prompt, host)
+        if not args.decode_once:
+            result["decode_q5_1"]["rows"] = rows_decode_leg(jev, np, L, lib, dmodel)
         dmodel.close()
         del dsynth
 

@@ -177,6 +177,23 @@ int jev_forward_tree(jev_ctx *ctx, const int32_t *trunk, int32_t n_trunk, const 
  * tokens_out receives the n_steps argmax ids (Kernels.ArgMax, lowest index on ties). */
 int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tokens_out);
 
+/* ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178, each step
+ * a ForwardRowsAsync of one token per row, MinistralModel.cs:272-294, with the
+ * rows layout TokenLayout.Rows :758-780): n_rows rows over `shared` shared
+ * positions, row r's slots from row_base[r] with row_length[r] tokens cached;
+ * every step feeds each row's last token (first[r] at step 0) and takes each
+ * row's argmax over the full vocabulary (lowest index on ties) as its next
+ * token.  The step runs as a replayed HIP graph with the per-row state on the
+ * device; tokens_out receives n_steps x n_rows ids, [step][row].  Every row
+ * runs all n_steps: the caller ends a row at its stop token by discarding
+ * what follows (rows are independent and the kernels batch-invariant, so a
+ * row's tokens do not depend on which other rows run, as long as two or more
+ * rows run -- a lone row takes the one-token path, QuantMatMul.cs:84).  The
+ * rows' slots over the whole run must stay clear of the shared prefix and of
+ * each other (JEV_EINVAL otherwise). */
+int jev_decode_rows_greedy(jev_ctx *ctx, int32_t shared, int32_t n_rows, const int32_t *row_base,
+                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out);
+
 /* JevstralDecider.DecideAsync margins (:306-308) and softmax(z/T) (:310-313):
  * verdicts is n_options x (n_yes + n_no). */
 int jev_margins(const float *verdicts, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature,

@@ -115,4 +115,69 @@ __device__ __forceinline__ float warp_max(float v)
     return v;
 }
 
+// Kernels.RmsNorm's statistics (Kernels.cs:25-60) for one row of D floats in
+// a workgroup of 256 threads: thread t owns the float4 groups g = t + 256 i
+// (i < NI), x[i] = h + the sum of the `nadd` K-split partials taken in split
+// order (Kernels.Add first), squares summed per thread in group order, then by
+// a fixed butterfly per wave and the four wave sums in order.  Returns
+// 1 / sqrt(sum / D + eps).  `wsum` is 4 floats of LDS.  Groups a thread does
+// not own (g >= D / 4) load a clamped neighbour and are left out of the sum.
+template <int NI, int NP>
+__device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *add4, int nadd, size_t pstride, int D,
+                                               float eps, float4 (&x)[NI], float *wsum)
+{
+    const int tid = threadIdx.x, ng = D >> 2;
+    float4 p[NP][NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        if (256 * i >= ng) break;
+        x[i] = h4[min(tid + 256 * i, ng - 1)];
+    }
+    if (add4) {
+#pragma unroll
+        for (int z = 0; z < NP; z++) {
+            if (z >= nadd) break;
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                if (256 * i >= ng) break;
+                p[z][i] = add4[z * pstride + min(tid + 256 * i, ng - 1)];
+            }
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        if (256 * i >= ng) break;
+        float4 v = x[i];
+        if (add4) {
+            float4 s4 = p[0][i];
+#pragma unroll
+            for (int z = 1; z < NP; z++) {
+                if (z >= nadd) break;
+                s4.x = s4.x + p[z][i].x;
+                s4.y = s4.y + p[z][i].y;
+                s4.z = s4.z + p[z][i].z;
+                s4.w = s4.w + p[z][i].w;
+            }
+            v.x = v.x + s4.x;
+            v.y = v.y + s4.y;
+            v.z = v.z + s4.z;
+            v.w = v.w + s4.w;
+        }
+        x[i] = v;
+        if (tid + 256 * i < ng) {
+            float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
+            ss = ss + q0;
+            ss = ss + q1;
+            ss = ss + q2;
+            ss = ss + q3;
+        }
+    }
+    ss = warp_sum(ss);
+    if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+    __syncthreads();
+    const float sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    return 1.0f / sqrtf(sum / (float)D + eps);
+}
+
 } // namespace jev

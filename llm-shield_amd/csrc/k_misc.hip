@@ -112,64 +112,21 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
     const int ng = a.D >> 2, nblk = a.D >> 5;
     float4 *h4 = (float4 *)(a.h + (size_t)row * a.D);
     const float4 *add4 = a.add ? (const float4 *)(a.add + (size_t)row * a.D) : nullptr;
-    const size_t pstride = a.add_stride >> 2;
-    float4 x[kNormIters], p[kNormParts][kNormIters], wv[kNormIters];
+    float4 x[kNormIters], wv[kNormIters];
     const float4 *w4 = (const float4 *)a.w;
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
         if (256 * i >= ng) break;
-        const int g = min(tid + 256 * i, ng - 1); // clamped: out-of-row lanes load and drop
-        x[i] = h4[g];
-        wv[i] = w4[g];
+        wv[i] = w4[min(tid + 256 * i, ng - 1)]; // clamped: out-of-row lanes load and drop
     }
-    if (add4) {
+    const float scale = row_rms_scale<kNormIters, kNormParts>(h4, add4, a.nadd, a.add_stride >> 2, a.D, a.eps, x, wsum);
+    if (add4 && a.store_h) {
 #pragma unroll
-        for (int z = 0; z < kNormParts; z++) {
-            if (z >= a.nadd) break;
-#pragma unroll
-            for (int i = 0; i < kNormIters; i++) {
-                if (256 * i >= ng) break;
-                const int g = min(tid + 256 * i, ng - 1);
-                p[z][i] = add4[z * pstride + g];
-            }
+        for (int i = 0; i < kNormIters; i++) {
+            if (256 * i >= ng) break;
+            if (tid + 256 * i < ng) h4[tid + 256 * i] = x[i];
         }
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < kNormIters; i++) {
-        if (256 * i >= ng) break;
-        const int g = tid + 256 * i;
-        float4 v = x[i];
-        if (add4) {
-            float4 s4 = p[0][i];
-#pragma unroll
-            for (int z = 1; z < kNormParts; z++) {
-                if (z >= a.nadd) break;
-                s4.x = s4.x + p[z][i].x;
-                s4.y = s4.y + p[z][i].y;
-                s4.z = s4.z + p[z][i].z;
-                s4.w = s4.w + p[z][i].w;
-            }
-            v.x = v.x + s4.x;
-            v.y = v.y + s4.y;
-            v.z = v.z + s4.z;
-            v.w = v.w + s4.w;
-            if (a.store_h && g < ng) h4[g] = v;
-        }
-        x[i] = v;
-        if (g < ng) {
-            float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
-            ss = ss + q0;
-            ss = ss + q1;
-            ss = ss + q2;
-            ss = ss + q3;
-        }
-    }
-    ss = warp_sum(ss);
-    if ((tid & 63) == 0) wsum[tid >> 6] = ss;
-    __syncthreads();
-    const float sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-    const float scale = 1.0f / sqrtf(sum / (float)a.D + a.eps);
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
         if (256 * i >= ng) break;
@@ -418,11 +375,20 @@ hipError_t launch_head_rows(const HeadRowsArgs &a, hipStream_t s)
 
 // ------------------------------------------------------------ argmax
 
-// Kernels.ArgMax (Kernels.cs:146): index of the largest element, lowest index
-// on ties.  Pass 1: one (value, index) per block; pass 2: one block over those.
+// Kernels.ArgMax (Kernels.cs:146) is TensorPrimitives.IndexOfMax: the first
+// NaN if there is one, else the largest element with +0 above -0, lowest
+// index on ties.  better() is that order as a reduction step, so any
+// reduction tree gives the same index, and the index is always in range.
+// Pass 1: one (value, index) per block; pass 2: one block over those.
 __device__ __forceinline__ void better(float &v, int &i, float v2, int i2)
 {
-    if (v2 > v || (v2 == v && i2 < i)) {
+    bool take;
+    if (v2 != v2) take = v == v || i2 < i;
+    else if (v != v) take = false;
+    else if (v2 != v) take = v2 > v;
+    else if (v2 == 0.f && signbit(v2) != signbit(v)) take = !signbit(v2);
+    else take = i2 < i;
+    if (take) {
         v = v2;
         i = i2;
     }
@@ -495,6 +461,55 @@ hipError_t launch_argmax_decode(const float *x, int n, float *sv, int32_t *si, i
     hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(256), 0, s, x, (const int32_t *)nullptr, n, sv, si);
     hipLaunchKernelGGL(argmax_decode_kernel, dim3(1), dim3(256), 0, s, (const float *)sv, (const int32_t *)si, blocks,
                        state, out);
+    return hipGetLastError();
+}
+
+// One greedy step of the rows layout (ReasoningDecider.cs:157-178): row r's
+// argmax over its logits (lowest index on ties, Kernels.ArgMax) becomes its
+// next input token and is recorded at out[rowstep[r] * n_rows + r]; the
+// row's cache slot, position and attention tile (one token each) advance by
+// one.  Each workgroup owns one row, so no two touch the same state.
+__global__ __launch_bounds__(256) void rows_step_kernel(const float *logits, int vocab, int n_rows, int32_t *tokens,
+                                                       int32_t *slot, int32_t *pos, AttnTile *tiles, int32_t *rowstep,
+                                                       int32_t *out)
+{
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int r = blockIdx.x;
+    const float *x = logits + (size_t)r * vocab;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int k = threadIdx.x; k < vocab; k += 256) better(v, idx, x[k], k);
+    bv[threadIdx.x] = v;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            float v1 = bv[threadIdx.x];
+            int i1 = bi[threadIdx.x];
+            better(v1, i1, bv[threadIdx.x + o], bi[threadIdx.x + o]);
+            bv[threadIdx.x] = v1;
+            bi[threadIdx.x] = i1;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int tok = bi[0];
+        tokens[r] = tok;
+        out[(size_t)rowstep[r] * n_rows + r] = tok;
+        rowstep[r] = rowstep[r] + 1;
+        slot[r] = slot[r] + 1;
+        pos[r] = pos[r] + 1;
+        if (tiles) tiles[r].slot0 = tiles[r].slot0 + 1;
+    }
+}
+
+hipError_t launch_rows_step(const float *logits, int vocab, int n_rows, int32_t *tokens, int32_t *slot, int32_t *pos,
+                            AttnTile *tiles, int32_t *rowstep, int32_t *out, hipStream_t s)
+{
+    if (n_rows <= 0 || vocab <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rows_step_kernel, dim3(n_rows), dim3(256), 0, s, logits, vocab, n_rows, tokens, slot, pos, tiles,
+                       rowstep, out);
     return hipGetLastError();
 }
 

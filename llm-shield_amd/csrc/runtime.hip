@@ -1593,6 +1593,128 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     return rc;
 }
 
+// ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178 through
+// ForwardRowsAsync, MinistralModel.cs:272-294): the rows-layout step captured
+// as a HIP graph and replayed.  The per-row tokens, slots, positions and
+// attention tiles live in the plan's device buffers and rows_step_kernel
+// advances them, so nothing returns to the host between steps.
+int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int32_t *row_base,
+                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out)
+{
+    int rc = check_ready(c);
+    if (rc) return rc;
+    if (n_rows <= 0 || n_steps <= 0 || shared < 0 || !row_base || !row_length || !first || !tokens_out)
+        return fail(JEV_EINVAL, "bad arguments");
+    // every row's slots over the whole run, [base, base + length + steps),
+    // clear of the shared prefix and of each other
+    std::vector<std::pair<int64_t, int64_t>> span(n_rows);
+    int64_t end_max = shared;
+    for (int r = 0; r < n_rows; r++) {
+        if (row_length[r] < 0 || row_base[r] < 0) return fail(JEV_EINVAL, "row %d: negative base or length", r);
+        if (first[r] < 0 || first[r] >= c->embd.rows)
+            return fail(JEV_EINVAL, "Token id %d is outside the %d-entry embedding table.", first[r], c->embd.rows);
+        span[r] = {row_base[r], (int64_t)row_base[r] + row_length[r] + n_steps};
+        end_max = std::max(end_max, span[r].second);
+        if (span[r].first < shared) return fail(JEV_EINVAL, "row %d starts at slot %d, inside the %d shared slots", r, row_base[r], shared);
+    }
+    if (end_max > (1 << 28)) return fail(JEV_EINVAL, "the rows reach slot %lld", (long long)end_max);
+    {
+        std::vector<std::pair<int64_t, int64_t>> sorted = span;
+        std::sort(sorted.begin(), sorted.end());
+        for (int r = 1; r < n_rows; r++)
+            if (sorted[r].first < sorted[r - 1].second)
+                return fail(JEV_EINVAL, "two rows' slots overlap within %d steps", n_steps);
+    }
+    CallScope call(c);
+    std::vector<int32_t> slot(n_rows), pos(n_rows), lo(n_rows, 0), hi(n_rows, shared), seg(n_rows), outs(n_rows);
+    int32_t end0 = shared;
+    for (int r = 0; r < n_rows; r++) {
+        slot[r] = row_base[r] + row_length[r];
+        pos[r] = shared + row_length[r];
+        seg[r] = row_base[r];
+        outs[r] = r;
+        end0 = std::max(end0, slot[r] + 1);
+    }
+    jev_layout lay{slot.data(), pos.data(), lo.data(), hi.data(), seg.data(), outs.data(), n_rows, end0};
+    rc = kv_ensure(c, (int)end_max);
+    if (rc) return rc;
+    Plan p;
+    rc = prepare(c, first, false, n_rows, &lay, JEV_OUT_FULL, nullptr, 0, p);
+    if (rc) return rc;
+    int max_limit = 0;
+    for (int r = 0; r < n_rows; r++) max_limit = std::max(max_limit, shared + row_length[r] + n_steps);
+    p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys; // grid for the longest step
+    rc = ensure_workspace(c, n_rows, p.n_out, JEV_OUT_FULL, p.max_chunks);
+    if (rc) return rc;
+    HIP_TRY(c->logits.ensure(std::max(c->logits.n, (size_t)n_rows * c->cfg.vocab)));
+    HIP_TRY(c->dec_state.ensure((size_t)n_rows * (n_steps + 1)));
+    int32_t *rowstep = c->dec_state.p, *out = c->dec_state.p + n_rows;
+    HIP_TRY(hipMemsetAsync(rowstep, 0, (size_t)n_rows * sizeof(int32_t), c->stream));
+    AttnTile *tiles = n_rows >= 2 ? c->tiles.p : nullptr;
+    auto step = [&]() -> int {
+        int r = enqueue_forward(c, p, JEV_OUT_FULL, 0, c->logits.p);
+        if (r) return r;
+        hipError_t e = launch_rows_step(c->logits.p, c->cfg.vocab, n_rows, const_cast<int32_t *>(p.d_tokens),
+                                        const_cast<int32_t *>(p.d_slot), const_cast<int32_t *>(p.d_pos), tiles, rowstep,
+                                        out, c->stream);
+        return e == hipSuccess ? JEV_OK : fail(JEV_EDEVICE, "rows step: %s", hipGetErrorString(e));
+    };
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (!c->profiling) {
+        HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        c->capturing = true;
+        rc = step();
+        c->capturing = false;
+        hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "graph capture: %s", hipGetErrorString(e));
+        if (!rc && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+            rc = fail(JEV_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    }
+    int launched = 0;
+    while (!rc && launched < n_steps) {
+        if (launched >= jev_ctx::kLeadLayers) {
+            hipError_t e = hipEventSynchronize(c->layer_ev[(launched - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]);
+            if (e != hipSuccess) {
+                rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
+                break;
+            }
+        }
+        if (call.cancelled()) {
+            rc = fail(JEV_ECANCELED, "rows decoding was cancelled after %d steps", launched);
+            break;
+        }
+        if (exec) {
+            hipError_t e = hipGraphLaunch(exec, c->stream);
+            if (e != hipSuccess) {
+                rc = fail(JEV_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+                break;
+            }
+        } else {
+            rc = step();
+            if (rc) break;
+        }
+        launched++;
+        hipError_t e = hipEventRecord(c->layer_ev[(launched - 1) % jev_ctx::kLayerEvents], c->stream);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
+    }
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
+    if (!rc && call.cancelled()) rc = fail(JEV_ECANCELED, "rows decoding was cancelled after %d steps", launched);
+    if (!rc || rc == JEV_ECANCELED) {
+        int32_t end = shared; // KvCache.Advance to the highest slot written
+        for (int r = 0; r < n_rows; r++) end = std::max(end, row_base[r] + row_length[r] + launched);
+        if (launched > 0) c->len = std::max(c->len, end);
+    }
+    if (!rc) {
+        e = hipMemcpy(tokens_out, out, sizeof(int32_t) * (size_t)n_steps * n_rows, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
+    }
+    return rc;
+}
+
 int jev_margins(const float *v, int32_t n_options, int32_t n_yes, int32_t n_no, float temperature, float *margins,
                 float *probs)
 {

@@ -8,7 +8,7 @@ from .synth import SEED, VERDICT_NO, VERDICT_YES, SynthModel, quantize, random_t
 from .weight import QuantWeight, get_matmul_strategy, quantize_activations, set_matmul_strategy
 from .prefix_cache import InvalidOperationError, SystemPromptCache
 from .decider import DecisionResult, TreeDecider, common_prefix, temperature_for
-from .reasoning import batched_greedy, decode_batch, plan_batches, row_bases
+from .reasoning import batched_greedy, decode_batch, index_of_max, plan_batches, row_bases
 
 __all__ = [
     "ArgumentError", "CancelledError", "DeviceSnapshot", "DataError", "GgufFile", "GgufTensorInfo", "JevError", "NotSupportedError",
@@ -18,5 +18,5 @@ __all__ = [
     "margins", "rope_table", "quantize", "random_tokens", "row_bytes", "synth_tensor", "MATMUL_AUTO", "MATMUL_FLOAT",
     "MATMUL_INTEGER", "get_matmul_strategy", "quantize_activations", "set_matmul_strategy",
     "InvalidOperationError", "SystemPromptCache", "DecisionResult", "TreeDecider", "common_prefix", "temperature_for",
-    "batched_greedy", "decode_batch", "plan_batches", "row_bases",
+    "batched_greedy", "decode_batch", "index_of_max", "plan_batches", "row_bases",
 ]

@@ -115,6 +115,7 @@ def lib():
         "jev_forward_tree": (c_int, [c_void_p, I32P, c_int32, I32P, I32P, c_int32, I32P, c_int32, F32P, c_size_t]),
         "jev_capture": (c_int, [c_void_p, I32P, c_int32, SINK, c_void_p, F32P, c_size_t]),
         "jev_decode_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P]),
+        "jev_decode_rows_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P, I32P, I32P, c_int32, I32P]),
         "jev_margins": (c_int, [F32P, c_int32, c_int32, c_int32, c_float, F32P, F32P]),
         "jev_cancel": (None, [c_void_p]),
         "jev_forward_device": (c_int, [c_void_p, c_void_p, c_int32, POINTER(Layout), c_int, I32P, c_int32, c_void_p]),
@@ -155,7 +156,7 @@ def check(rc: int) -> None:
 EXPORTED = [
     "jev_last_error", "jev_create", "jev_destroy", "jev_bind_tensor", "jev_finalize", "jev_kv_length",
     "jev_kv_capacity", "jev_kv_reserve", "jev_kv_truncate", "jev_kv_reset", "jev_kv_snapshot", "jev_kv_restore",
-    "jev_forward", "jev_forward_tree", "jev_decode_greedy", "jev_margins", "jev_cancel", "jev_forward_device",
+    "jev_forward", "jev_forward_tree", "jev_decode_greedy", "jev_decode_rows_greedy", "jev_margins", "jev_cancel", "jev_forward_device",
     "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
     "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations", "jev_rope_table",

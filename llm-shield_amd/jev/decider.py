@@ -63,7 +63,8 @@ class DecisionResult:
     @property
     def best(self) -> int:
         """Index of the most probable option (Kernels.ArgMax: the first maximum)."""
-        return int(np.argmax(self.probabilities))
+        from .reasoning import index_of_max
+        return index_of_max(self.probabilities)
 
 
 @dataclass

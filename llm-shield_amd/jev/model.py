@@ -384,6 +384,20 @@ class MinistralModel:
         L.check(self._lib.jev_decode_greedy(self._h, first, steps, _ptr(out, ctypes.c_int32)))
         return out
 
+    def decode_rows_greedy(self, shared: int, row_base, row_length, first, steps: int) -> np.ndarray:
+        """ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178) as a
+        replayed device graph: every row runs `steps` one-token passes fed with
+        its own argmax.  Returns the tokens as [steps][rows]."""
+        base, length, fst = _i32(row_base), _i32(row_length), _i32(first)
+        n = len(base)
+        if len(length) != n or len(fst) != n:
+            raise L.ArgumentError(L.JEV_EINVAL, "row_base, row_length and first must have one entry per row")
+        out = np.empty((steps, n), np.int32)
+        L.check(self._lib.jev_decode_rows_greedy(self._h, shared, n, _ptr(base, ctypes.c_int32),
+                                                 _ptr(length, ctypes.c_int32), _ptr(fst, ctypes.c_int32), steps,
+                                                 _ptr(out, ctypes.c_int32)))
+        return out
+
     def forward_capture(self, tokens):
         """ForwardAsync(tokens, capture, options) (MinistralModel.cs:157-160): the last
         token's logits and every tensor an IActivationSink observes, as

@@ -49,16 +49,35 @@ def row_bases(lengths: Sequence[int], max_new_tokens: int) -> List[int]:
     return bases
 
 
-def _argmax(logits: np.ndarray) -> int:
-    return int(np.argmax(logits))  # Kernels.ArgMax: the first maximum
+def index_of_max(x) -> int:
+    """Kernels.ArgMax (Kernels.cs:146), TensorPrimitives.IndexOfMax: the first
+    NaN if there is one, else the largest value with +0 above -0, the lowest
+    index on ties (the order the device argmax reduces in)."""
+    x = np.asarray(x, np.float32).reshape(-1)
+    nan = np.flatnonzero(np.isnan(x))
+    if nan.size:
+        return int(nan[0])
+    top = np.flatnonzero(x == x.max())
+    if x[top[0]] == 0:
+        pos = top[~np.signbit(x[top])]
+        if pos.size:
+            return int(pos[0])
+    return int(top[0])
+
+
+_argmax = index_of_max
 
 
 def decode_batch(model, prompts: Sequence[Sequence[int]], max_new_tokens: int,
-                 stop_tokens: Sequence[int] = ()) -> List[List[int]]:
+                 stop_tokens: Sequence[int] = (), graph: bool = False, chunk: int = 32) -> List[List[int]]:
     """RunBatchAsync's token loop (ReasoningDecider.cs:134-174) for one batch.
 
     Returns each row's decoded tokens, a stop token included when one ended
-    the row.  Leaves the rows in the cache (the caller may continue them)."""
+    the row.  Leaves the rows in the cache (the caller may continue them).
+
+    graph=True runs the loop as replayed device graphs of up to `chunk` steps
+    (jev_decode_rows_greedy) and checks stop tokens between chunks; the
+    tokens are the ones the step-by-step loop gives (see _decode_graph)."""
     if max_new_tokens < 1:
         raise L.ArgumentError(L.JEV_EINVAL, "max_new_tokens must be at least 1.")
     if any(len(p) == 0 for p in prompts):
@@ -75,6 +94,12 @@ def decode_batch(model, prompts: Sequence[Sequence[int]], max_new_tokens: int,
         nxt[r] = _argmax(logits[0])
     out: List[List[int]] = [[] for _ in range(rows)]
     done = [False] * rows
+    if graph:
+        for r in range(rows):
+            out[r].append(nxt[r])
+            done[r] = nxt[r] in stops
+        _decode_graph(model, bases, length, nxt, out, done, stops, max_new_tokens, chunk)
+        return out
     for step in range(max_new_tokens):
         active = []
         for r in range(rows):
@@ -95,13 +120,53 @@ def decode_batch(model, prompts: Sequence[Sequence[int]], max_new_tokens: int,
     return out
 
 
+def _decode_graph(model, bases, length, nxt, out, done, stops, max_new_tokens: int, chunk: int) -> None:
+    """The token loop in chunks of replayed steps.  Every row of a chunk runs
+    every step, a stopped one too (its extra tokens are dropped and its slots
+    beyond its length are never read).  The kernels are batch invariant, so a
+    row's tokens do not depend on which other rows share its passes, except
+    that one row alone takes the one-token path (QuantMatMul.cs:84, below
+    PanelMinTokens): when the step-by-step loop would run the last surviving
+    row alone, its tokens from that step on are dropped and it continues as
+    a chunk of one row, rewriting those slots."""
+    if chunk < 1:
+        raise L.ArgumentError(L.JEV_EINVAL, "chunk must be at least 1.")
+    rows = len(out)
+    while True:
+        active = [r for r in range(rows) if not done[r] and len(out[r]) < max_new_tokens]
+        if not active:
+            return
+        n = min(chunk, max_new_tokens - len(out[active[0]]))
+        toks = model.decode_rows_greedy(0, [bases[r] for r in active], [length[r] for r in active],
+                                        [nxt[r] for r in active], n)
+        alive = list(range(len(active)))
+        for k in range(n):
+            if len(active) >= 2 and len(alive) == 1:
+                break  # the survivor runs alone from here: next chunk
+            still = []
+            for i in alive:
+                r = active[i]
+                t = int(toks[k, i])
+                length[r] += 1
+                nxt[r] = t
+                out[r].append(t)
+                if t in stops:
+                    done[r] = True
+                else:
+                    still.append(i)
+            alive = still
+            if not alive:
+                break
+
+
 def batched_greedy(model, prompts: Sequence[Sequence[int]], max_new_tokens: int, stop_tokens: Sequence[int] = (),
-                   max_rows: int = MAX_ROWS, kv_token_budget: int = KV_TOKEN_BUDGET) -> List[List[int]]:
+                   max_rows: int = MAX_ROWS, kv_token_budget: int = KV_TOKEN_BUDGET, graph: bool = False,
+                   chunk: int = 32) -> List[List[int]]:
     """Every prompt's greedy continuation, decoded in batches of rows
     (DecideAsync + RunBatchAsync); the cache is reset after each batch."""
     results: List[List[int]] = [[] for _ in prompts]
     for batch in plan_batches([len(p) for p in prompts], max_new_tokens, max_rows, kv_token_budget):
-        got = decode_batch(model, [prompts[i] for i in batch], max_new_tokens, stop_tokens)
+        got = decode_batch(model, [prompts[i] for i in batch], max_new_tokens, stop_tokens, graph, chunk)
         for i, toks in zip(batch, got):
             results[i] = toks
         model.reset_kv_cache()

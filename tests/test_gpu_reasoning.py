@@ -43,3 +43,82 @@ def test_a_stop_token_ends_its_row_only(gpu, synth):
     for f, g in zip(free, got):
         assert g == (f[:f.index(stop) + 1] if stop in f else f)
     assert len(got[0]) <= 2
+
+
+def _rows_stepwise(m, shared, bases, lengths, first, steps):
+    """The loop jev_decode_rows_greedy replays, one forward_rows call per step."""
+    lengths, nxt, out = list(lengths), list(first), []
+    for _ in range(steps):
+        logits = m.forward_rows(shared, bases, lengths, [[t] for t in nxt])
+        lengths = [n + 1 for n in lengths]
+        nxt = [jev.reasoning.index_of_max(z) for z in logits]
+        out.append(nxt)
+    return np.array(out, np.int32)
+
+
+def test_rows_graph_is_the_step_by_step_loop_over_a_shared_prefix(gpu, synth):
+    trunk = jev.random_tokens(21, 2048, 70)
+    prompts = [list(jev.random_tokens(n, 2048, 71 + n)) for n in (5, 11, 2)]
+    bases = [40, 80, 120]
+    steps = 13
+    with synth.open(0) as m:
+        def start():
+            m.reset_kv_cache()
+            m.prefill(trunk)
+            logits = m.forward_rows(len(trunk), bases, [0, 0, 0], prompts)
+            return [jev.reasoning.index_of_max(z) for z in logits]
+        first = start()
+        g = m.decode_rows_greedy(len(trunk), bases, [len(p) for p in prompts], first, steps)
+        assert m.cached_token_count >= bases[2] + len(prompts[2]) + steps
+        assert start() == first
+        s = _rows_stepwise(m, len(trunk), bases, [len(p) for p in prompts], first, steps)
+    assert g.shape == (steps, 3)
+    assert np.array_equal(g, s)
+    # row 1 teacher-forced through the oracle on trunk + its prompt alone
+    ref = oracle.OracleModel(synth.config).bind_synth(synth)
+    e = ref.forward(list(trunk) + prompts[1])
+    assert e[first[1]] >= e.max() - 2e-3 * max(1.0, abs(float(e.max())))
+    for t_in, t_out in zip([first[1]] + list(g[:-1, 1]), g[:, 1]):
+        e = ref.forward([int(t_in)])
+        assert e[t_out] >= e.max() - 2e-3 * max(1.0, abs(float(e.max())))
+
+
+def test_one_row_is_the_one_token_decode(gpu, synth):
+    # a lone row takes the one-token path: the same kernels and keys as jev_decode_greedy
+    tokens = jev.random_tokens(30, 2048, 75)
+    with synth.open(0) as m:
+        m.reset_kv_cache()
+        m.prefill(tokens)
+        want = m.decode_greedy(int(tokens[-1]), 9)
+        m.reset_kv_cache()
+        m.prefill(tokens)
+        got = m.decode_rows_greedy(0, [0], [len(tokens)], [int(tokens[-1])], 9)
+    assert np.array_equal(got[:, 0], want)
+
+
+@pytest.mark.parametrize("chunk", [3, 32])
+def test_graph_batches_give_the_step_by_step_tokens(gpu, synth, chunk):
+    prompts = [list(jev.random_tokens(n, 2048, 80 + n)) for n in (6, 13, 9, 17)]
+    with synth.open(0) as m:
+        free = jev.batched_greedy(m, prompts, 10)
+        assert jev.batched_greedy(m, prompts, 10, graph=True, chunk=chunk) == free
+        # rows stop one after another until one runs alone
+        stops = {free[0][2], free[1][4], free[2][5]} - set(free[3])
+        want = jev.batched_greedy(m, prompts, 10, stop_tokens=stops)
+        got = jev.batched_greedy(m, prompts, 10, stop_tokens=stops, graph=True, chunk=chunk)
+    assert got == want
+
+
+def test_rows_graph_rejects_rows_that_meet(gpu, synth):
+    with synth.open(0) as m:
+        m.reset_kv_cache()
+        m.prefill(jev.random_tokens(8, 2048, 90))
+        n = m.cached_token_count
+        for shared, bases, lengths in [(8, [10, 20], [7, 2]),     # row 0 runs into row 1 within 4 steps
+                                       (8, [4, 30], [0, 0]),      # row 0 inside the shared prefix
+                                       (8, [30, 30], [0, 0])]:
+            with pytest.raises(jev.ArgumentError):
+                m.decode_rows_greedy(shared, bases, lengths, [1, 2], 4)
+        with pytest.raises(jev.ArgumentError):
+            m.decode_rows_greedy(8, [10, 40], [0, 0], [1, 5000], 4)  # outside the embedding table
+        assert m.cached_token_count == n

@@ -36,6 +36,41 @@ class RowsModel:
         return out
 
 
+class GraphRowsModel(RowsModel):
+    """RowsModel plus decode_rows_greedy.  A pass of one token in total takes
+    another next-token rule, as a lone row takes the one-token path on the
+    device, so a loop that runs the last row with others where the step-by-step
+    loop runs it alone gives other tokens."""
+
+    def __init__(self):
+        super().__init__()
+        self.graph_calls = []
+
+    @staticmethod
+    def rule(t, alone):
+        return (5 * t + 1) % V if alone else (7 * t + 3) % V
+
+    def forward_rows(self, shared, row_base, row_length, row_tokens, vocab_rows=None):
+        self.calls.append((list(row_base), list(row_length), [list(t) for t in row_tokens]))
+        alone = sum(len(t) for t in row_tokens) == 1
+        out = []
+        for toks in row_tokens:
+            z = np.zeros(V, np.float32)
+            z[self.rule(toks[-1], alone)] = 1.0
+            out.append(z)
+        return out
+
+    def decode_rows_greedy(self, shared, row_base, row_length, first, steps):
+        assert shared == 0
+        self.graph_calls.append((list(row_base), list(row_length), list(first), steps))
+        out = np.empty((steps, len(first)), np.int32)
+        t = list(first)
+        for k in range(steps):
+            t = [self.rule(x, len(first) == 1) for x in t]
+            out[k] = t
+        return out
+
+
 def _expected(prompt, n, stops):
     seq, t = [], prompt[-1]
     for _ in range(n):
@@ -89,3 +124,45 @@ def test_rejections():
         R.decode_batch(RowsModel(), [[1], []], 2)
     with pytest.raises(jev.ArgumentError):
         R.decode_batch(RowsModel(), [[1]], 0)
+
+
+def test_index_of_max_follows_index_of_max():
+    assert R.index_of_max([1.0, 3.0, 3.0, 2.0]) == 1                 # lowest index on ties
+    assert R.index_of_max([1.0, np.nan, 5.0, np.nan]) == 1           # the first NaN
+    assert R.index_of_max([np.nan, np.nan]) == 0
+    assert R.index_of_max([-0.0, 0.0, -1.0]) == 1                    # +0 above -0
+    assert R.index_of_max([0.0, -0.0]) == 0
+    assert R.index_of_max([-np.inf, -np.inf]) == 0
+    assert R.index_of_max([-5.0, -0.0, -0.0]) == 1
+
+
+@pytest.mark.parametrize("chunk", [1, 2, 3, 32])
+@pytest.mark.parametrize("stop_on", [None, "first", "late", "all_but_one"])
+def test_graph_chunks_give_the_step_by_step_tokens(chunk, stop_on):
+    prompts = [[1, 2, 3], [4, 5], [6], [11, 12, 13, 14]]
+    n = 9
+    free = R.decode_batch(GraphRowsModel(), prompts, n)
+    stops = set()
+    if stop_on == "first":
+        stops = {free[1][0]}
+    elif stop_on == "late":
+        stops = {free[2][4]}
+    elif stop_on == "all_but_one":  # rows stop one by one; the last runs alone for a while
+        stops = {free[0][1], free[1][2], free[2][3]} - set(free[3])
+    want = R.decode_batch(GraphRowsModel(), prompts, n, stop_tokens=stops)
+    m = GraphRowsModel()
+    got = R.decode_batch(m, prompts, n, stop_tokens=stops, graph=True, chunk=chunk)
+    assert got == want
+    bases = R.row_bases([len(p) for p in prompts], n)
+    for base, length, first, steps in m.graph_calls:
+        assert 1 <= steps <= chunk
+        for b, ln in zip(base, length):  # each row stays inside its own slots
+            r = bases.index(b)
+            assert len(prompts[r]) <= ln and ln + steps <= len(prompts[r]) + n - 1
+    if stop_on == "all_but_one" and len(stops) == 3:
+        assert any(len(c[0]) == 1 for c in m.graph_calls)  # the survivor ran alone
+
+
+def test_graph_mode_rejects_a_zero_chunk():
+    with pytest.raises(jev.ArgumentError):
+        R.decode_batch(GraphRowsModel(), [[1], [2]], 3, graph=True, chunk=0)
