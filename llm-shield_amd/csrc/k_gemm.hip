@@ -743,6 +743,240 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     }
 }
 
+// Skinny variant for M <= 16 (one row group: the reasoning decider's rows,
+// short branches).  The B-direct grid at such M is N / 128 x splits
+// workgroups -- 96 for a 3072-row projection split 4 -- and leaves most of the
+// chip's load bandwidth idle.  Here each wave owns one 16-row weight group
+// (SwiGLU: the gate and the up group of the same outputs) and the workgroup's
+// four waves one K split, 8x the waves of B-direct.  Each wave streams its
+// weights through its own U-stage register ring; the activation fragments
+// (and Q5_1 block sums), the same for all four waves, are staged into LDS
+// once per workgroup in chunks of CH stages, double buffered, with one
+// barrier per chunk: loaded into registers at the top of the chunk before,
+// written to LDS at its end.  (Direct-to-LDS loads would save the registers,
+// but the compiler then drains every outstanding load before the first LDS
+// read after them, the weight ring included, once per chunk.)  Per output it issues exactly
+// gemm_bd_kernel's sequence: per block p = mfma(x_hi, q); p = mfma(x_lo, q,
+// p); acc = fma(d, p, acc) (+ fma(m, sum x, acc)), blocks ascending within the
+// split, the same clamped operands for an odd last block -- so its results
+// are the same bits.
+template <int TYPE, int MODE, int U, int CH>
+__global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngroups, int nq)
+{
+    constexpr int TN = MODE == kGemmSwiGlu ? 2 : 1;
+    constexpr int NB = (TYPE == kQ5_1 ? 3 : 2) * TN; // weight loads per stage
+    static_assert(CH % U == 0, "ring slots restart at every chunk");
+    static_assert(CH * NB + CH + 1 <= 63, "outstanding loads beyond the vmcnt range");
+    __shared__ __attribute__((aligned(16))) uint4 As[2][CH * 4 * 64]; // [stage][block][part][lane]
+    __shared__ __attribute__((aligned(16))) float Xs[2][TYPE == kQ5_1 ? CH * 2 * 16 : 4]; // [block][row]
+
+    // Every index below is wave-uniform and kept in scalar registers: the
+    // integer divisions are vector-ALU sequences, and left as vector values
+    // their results would drag all the per-stage address arithmetic onto the
+    // vector ALU with the decode and the scale FMAs.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int z = __builtin_amdgcn_readfirstlane((int)blockIdx.x / nq), q = blockIdx.x - z * nq;
+    const int g = q * 4 + wave;              // this wave's row group; past ngroups: loads only
+    const int gl = min(g, ngroups - 1);
+    const int M = a.M, K = a.K, nblk = K >> 5;
+    const int nb_per = __builtin_amdgcn_readfirstlane(gemm_split_blocks(nblk, a.ksplit));
+    const int kb_begin = z * nb_per;
+    const int nb = min(nblk - kb_begin, nb_per);
+    const int nstage = (nb + 1) >> 1;
+    const int nchunk = __builtin_amdgcn_readfirstlane((nstage + CH - 1) / CH);
+
+    const rsrc_t ra = make_rsrc(a.xt, (uint32_t)nblk * 2048); // row group 0 of the operand tiles
+    rsrc_t rs;
+    if (TYPE == kQ5_1) rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
+
+    // weights: tile n of this wave
+    rsrc_t rq[TN], rd[TN], rh[TN];
+    int btile0[TN];
+    int seg_store = 0, start_store = 0;
+    const uint32_t vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
+#pragma unroll
+    for (int n = 0; n < TN; n++) {
+        int seg, rgw;
+        if (MODE == kGemmSwiGlu) {
+            seg = n;
+            rgw = gl;
+        } else {
+            int s0 = 0, start = 0;
+            while (s0 + 1 < a.nseg && gl * 16 >= start + a.seg[s0].rows) {
+                start += a.seg[s0].rows;
+                s0++;
+            }
+            seg = s0;
+            rgw = (gl * 16 - start) / 16;
+            seg_store = s0;
+            start_store = start;
+        }
+        seg = __builtin_amdgcn_readfirstlane(seg);
+        const QWeight &wt = a.seg[seg];
+        const int KP = tile_kpairs(wt.cols), RG = tile_rows(wt.rows);
+        const uint32_t tiles = (uint32_t)RG * KP;
+        rq[n] = make_rsrc(wt.qs, tiles * tile_qs_bytes(TYPE));
+        rd[n] = make_rsrc(wt.d, tiles * tile_d_bytes(TYPE));
+        if (TYPE == kQ5_1) rh[n] = make_rsrc(wt.qh, tiles * 128);
+        btile0[n] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + (kb_begin >> 1));
+    }
+    auto load_b = [&](int st, BChunk (&br)[TN]) __attribute__((always_inline)) {
+        st = min(st, nstage - 1);
+#pragma unroll
+        for (int n = 0; n < TN; n++) {
+            const int tile = __builtin_amdgcn_readfirstlane(btile0[n] + st);
+            if (TYPE == kQ8_0) {
+                br[n].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[n], vq, tile * 1024, 0));
+            } else {
+                uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[n], vq, tile * 512, 0));
+                br[n].q = make_uint4(v.x, v.y, 0u, 0u);
+            }
+            if (TYPE == kQ5_1) {
+                const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[n], 2 * vd, tile * 128, 0));
+                br[n].d = dm.x;
+                br[n].m = dm.y;
+                br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
+            } else {
+                br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
+            }
+        }
+    };
+    // Chunk c's activation fragments: this wave's CH of the chunk's 4 * CH,
+    // fragment f = stage * 4 + block * 2 + part, one KiB each.
+    auto load_a = [&](int c, uint4 (&ar)[CH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int f = wave * CH + i;
+            const int st = min(c * CH + (f >> 2), nstage - 1);
+            const int kblk = kb_begin + min(2 * st + ((f >> 1) & 1), nb - 1);
+            // the offset is wave-uniform; as a vector value it would cost a one-pass loop per load
+            const int soff = __builtin_amdgcn_readfirstlane((kblk * 2 + (f & 1)) * 1024);
+            ar[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, lane * 16, soff, 0));
+        }
+    };
+    auto store_a = [&](int buf, const uint4 (&ar)[CH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < CH; i++) As[buf][(wave * CH + i) * 64 + lane] = ar[i];
+    };
+    // Chunk c's block sums, thread t: block t / 16 of the chunk, row t % 16
+    // (the address gemm_bd_kernel reads for that row and block).
+    auto load_xs = [&](int c) __attribute__((always_inline)) -> float {
+        if (TYPE != kQ5_1 || tid >= CH * 32) return 0.f;
+        const int bl = tid >> 4, st = min(c * CH + (bl >> 1), nstage - 1);
+        const uint32_t off = ((uint32_t)(tid & 15) * nblk + kb_begin + 2 * st + (bl & 1)) * 4;
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+    };
+
+    floatx4 acc[TN];
+#pragma unroll
+    for (int n = 0; n < TN; n++) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](int st, int buf, int sl, const BChunk (&br)[TN]) __attribute__((always_inline)) {
+        const bool second = 2 * st + 1 < nb;
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            const uint32_t live = bb == 0 || second ? ~0u : 0u;
+            const half8_t ah = __builtin_bit_cast(half8_t, As[buf][(sl * 4 + bb * 2 + 0) * 64 + lane]);
+            const half8_t al = __builtin_bit_cast(half8_t, As[buf][(sl * 4 + bb * 2 + 1) * 64 + lane]);
+            floatx4 xs4;
+            if (TYPE == kQ5_1) xs4 = *(const floatx4 *)&Xs[buf][(sl * 2 + bb) * 16 + 4 * (lane >> 4)];
+#pragma unroll
+            for (int n = 0; n < TN; n++) {
+                const half8_t bf = decode_b_frag<TYPE>(br[n], bb);
+                const float dv = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d))) & live);
+                float mv = 0.f;
+                if (TYPE == kQ5_1)
+                    mv = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m))) & live);
+                floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf, p, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float v = fmaf(dv, p[r], acc[n][r]);
+                    if (TYPE == kQ5_1) v = fmaf(mv, xs4[r], v);
+                    acc[n][r] = v;
+                }
+            }
+        }
+    };
+
+    // ---- pipeline.  Issue order per chunk c: the activations and block sums
+    // of chunk c + 1 (registers, written to the other LDS buffer at the end of
+    // chunk c), then one weight stage per stage of chunk c, U stages ahead.
+    BChunk br[U][TN];
+    uint4 ar[CH];
+    float xr = load_xs(0);
+    load_a(0, ar);
+#pragma unroll
+    for (int t = 0; t < U; t++) load_b(t, br[t]);
+    store_a(0, ar);
+    if (TYPE == kQ5_1 && tid < CH * 32) Xs[0][tid] = xr;
+    // Unconditional, so every chunk issues the same loads (the last one
+    // re-reads clamped stages into a buffer nobody reads): with a branch
+    // around them the compiler's wait counts at the chunk top assume the
+    // shorter path and wait on the activation loads just issued.
+    for (int c = 0; c < nchunk; c++) {
+        const int buf = c & 1;
+        __syncthreads(); // chunk c staged by everyone; chunk c - 1's buffers are free
+        xr = load_xs(c + 1);
+        load_a(c + 1, ar);
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int st = c * CH + j;
+            if (st < nstage) compute(st, buf, j, br[j % U]);
+            load_b(st + U, br[j % U]);
+        }
+        store_a(buf ^ 1, ar);
+        if (TYPE == kQ5_1 && tid < CH * 32) Xs[buf ^ 1][tid] = xr;
+    }
+
+    // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16].
+    if (g >= ngroups) return;
+    const int row_base = 4 * (lane >> 4);
+    if (MODE == kGemmStore) {
+        const QWeight &ws = a.seg[seg_store];
+        if (g * 16 - start_store + (lane & 15) >= ws.rows) return;
+        float *y = a.y + (size_t)z * M * a.ldy + g * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (row_base + r < M) y[(size_t)(row_base + r) * a.ldy] = acc[0][r];
+    } else {
+        const int ld = a.seg[0].rows;
+        const int col = g * 16 + (lane & 15);
+        if (col >= ld) return;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = row_base + r;
+            if (row >= M) continue;
+            // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g).
+            const float gv = acc[0][r], u = acc[1][r];
+            const float gu = gv * u;
+            const float e = expf(-gv);
+            const float sg = 1.0f / (1.0f + e);
+            const float v = sg * gu;
+            uint16_t hi, lo;
+            split_f16(v, hi, lo);
+            a.ot[xt_index(row, col, ld >> 5, 0)] = hi;
+            a.ot[xt_index(row, col, ld >> 5, 1)] = lo;
+        }
+    }
+}
+
+template <int TYPE, int MODE, int U, int CH>
+static hipError_t launch_skinny(const GemmArgs &a, hipStream_t s)
+{
+    int ngroups;
+    if (MODE == kGemmSwiGlu) {
+        ngroups = a.seg[0].rows / 16;
+    } else {
+        // every segment but the last is a whole number of 16-row groups
+        int ntot = 0;
+        for (int i = 0; i < a.nseg; i++) ntot += a.seg[i].rows;
+        ngroups = (ntot + 15) / 16;
+    }
+    const int nq = (ngroups + 3) / 4;
+    hipLaunchKernelGGL((gemm_skinny_kernel<TYPE, MODE, U, CH>), dim3(nq * a.ksplit), dim3(256), 0, s, a, ngroups, nq);
+    return hipGetLastError();
+}
+
 // gm_cap: M tiles per group of the tile order (the tiles of a group that share
 // an N column run on one XCD, so its L2 serves their common weight tile).
 template <int TYPE, int MODE, int TM, int TN, int PD, int OCC>
@@ -796,6 +1030,10 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
     // the store-mode segments to split on 256-row boundaries.
     bool bd_ok = true;
     for (int i = 0; i + 1 < a.nseg; i++) bd_ok = bd_ok && a.seg[i].rows % 256 == 0;
+    // One row group (the reasoning decider's rows, short branches): one wave
+    // per weight row group, 1.5-2x the B-direct kernel there (12 rows of the
+    // Q5_1 3B shape: 2.1 against 3.6 ms of GEMM per step)
+    if (a.M <= 16) return launch_skinny<TYPE, MODE, 4, 8>(a, s);
     if (a.M <= 512) {
         // SwiGLU (9216 rows at 256 tokens: 1152 workgroups): built for five
         // resident workgroups per CU (80 VGPRs, six fit) so they all run in

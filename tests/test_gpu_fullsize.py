@@ -57,7 +57,9 @@ def test_full_shape_logits_and_decode_match_oracle(model, synth):
 
 def test_full_shape_tree_equals_branches_alone_bitwise(model):
     trunk = jev.random_tokens(600, VOCAB, 6)
-    branches = [jev.random_tokens(48, VOCAB, 60 + i) for i in range(9)]
+    # seven 48-token branches and two short ones: a short branch alone runs the
+    # small-batch GEMM (2..16 tokens), inside the tree the large-batch one
+    branches = [jev.random_tokens(n, VOCAB, 60 + i) for i, n in enumerate([48] * 7 + [5, 16])]
     model.reset_kv_cache()
     model.prefill(trunk)
     alone = []
