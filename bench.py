@@ -392,6 +392,8 @@ def main():
     ap.add_argument("--no-batched", action="store_true", help="skip the batched Q4_0 decisions leg")
     ap.add_argument("--no-matmul", action="store_true", help="skip the single-matmul leg")
     ap.add_argument("--decode-once", action="store_true", help="one timed decode run, no warm-up or profiled pass")
+    ap.add_argument("--decode-ungraphed", action="store_true",
+                    help="one decode run with every kernel launched on its own (no HIP graph), for counter passes")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy (byte-counter calibration) and exit")
     ap.add_argument("--blas-ref", action="store_true",
@@ -668,12 +670,15 @@ def main():
             out = dmodel.decode_greedy(int(prompt[-1]), n_dec)
             return time.perf_counter() - t, out
 
-        if not args.decode_once:
+        once = args.decode_once or args.decode_ungraphed
+        if not once:
             decode_run()
+        if args.decode_ungraphed:
+            L.check(lib.jev_profile_enable(dh, 1))  # the decode loop then launches kernel by kernel
         dt, toks = decode_run()
         ms_tok = dt / n_dec * 1e3
         gv = da = (0, 0.0, 0.0, 0.0)
-        if not args.decode_once:
+        if not once:
             L.check(lib.jev_kv_reset(dh))
             dmodel.prefill(prompt)
             L.check(lib.jev_sync(dh))
@@ -697,7 +702,7 @@ def main():
         }
         if not args.no_cpu:
             result["decode_q5_1"]["cpu_baseline"] = decode_cpu_baseline(jev, dsynth, dcfg, prompt, host)
-        if not args.decode_once:
+        if not once:
             result["decode_q5_1"]["rows"] = rows_decode_leg(jev, np, L, lib, dmodel)
         dmodel.close()
         del dsynth
