@@ -59,8 +59,10 @@ def host_info():
     except OSError:
         pass
     host_isa = "AVX-512" if "avx512f" in flags else ("AVX2" if "avx2" in flags else "x86-64")
+    oracle_isa = ("x86-64-v3 (AVX2 + FMA; gcc -O3 -march=x86-64-v3), the panel GEMM in 512-bit tiles"
+                  if host_isa == "AVX-512" else "x86-64-v3 (AVX2 + FMA; gcc -O3 -march=x86-64-v3)")
     return {"cpu": model, "cpus_visible": cpus, "threads": max(1, min(16, cpus)),
-            "host_isa": host_isa, "oracle_isa": "x86-64-v3 (AVX2 + FMA; gcc -O3 -march=x86-64-v3)"}
+            "host_isa": host_isa, "oracle_isa": oracle_isa}
 
 
 def time_best(work, warmups=1, repeats=3, min_sample=0.25, setup=None):

@@ -24,8 +24,19 @@
 #endif
 
 static int g_threads = 0;
+static int g_vector_bits = 0; /* 0: 512 when the host has AVX-512F, else 256 */
 
 void orc_set_threads(int n) { g_threads = n; }
+void orc_set_vector_bits(int bits) { g_vector_bits = bits; }
+int orc_get_vector_bits(void)
+{
+#if defined(__x86_64__)
+    if (g_vector_bits == 512 || g_vector_bits == 256) return g_vector_bits;
+    return __builtin_cpu_supports("avx512f") ? 512 : 256;
+#else
+    return 256;
+#endif
+}
 int orc_get_threads(void)
 {
 #ifdef _OPENMP
@@ -261,6 +272,55 @@ static int panel_supports(int type, int rows, int cols)
     return rows % PANEL == 0 && cols % bs == 0 && (cols <= KBLOCK || KBLOCK % bs == 0);
 }
 
+/* PanelGemm's 512-bit tiles (Tile512x6 / Tile512x1, PanelGemm.cs:245-318):
+ * the 64 outputs of a panel as four 16-float vectors per token, six tokens at
+ * a time in 24 accumulator registers.  Every output is the same fused chain
+ * over k ascending as the portable loops below (the 256-bit path), so both
+ * give the same bits; PanelGemm picks 512 bits when the JIT accelerates them
+ * (VectorBits, :50-63), and so does the oracle (orc_get_vector_bits). */
+#if defined(__x86_64__)
+#include <immintrin.h>
+__attribute__((target("avx512f"))) static void tile6_512(const float *x, int64_t ldx, const float *p, int kc,
+                                                         float *y, int64_t ldy, int acc)
+{
+    __m512 c[ROWBLK][4];
+    for (int i = 0; i < ROWBLK; i++)
+        for (int j = 0; j < 4; j++) c[i][j] = acc ? _mm512_loadu_ps(y + i * ldy + 16 * j) : _mm512_setzero_ps();
+    for (int k = 0; k < kc; k++) {
+        const float *w = p + (int64_t)k * PANEL;
+        const __m512 b0 = _mm512_loadu_ps(w), b1 = _mm512_loadu_ps(w + 16), b2 = _mm512_loadu_ps(w + 32),
+                     b3 = _mm512_loadu_ps(w + 48);
+        for (int i = 0; i < ROWBLK; i++) {
+            const __m512 sv = _mm512_set1_ps(x[i * ldx + k]);
+            c[i][0] = _mm512_fmadd_ps(sv, b0, c[i][0]);
+            c[i][1] = _mm512_fmadd_ps(sv, b1, c[i][1]);
+            c[i][2] = _mm512_fmadd_ps(sv, b2, c[i][2]);
+            c[i][3] = _mm512_fmadd_ps(sv, b3, c[i][3]);
+        }
+    }
+    for (int i = 0; i < ROWBLK; i++)
+        for (int j = 0; j < 4; j++) _mm512_storeu_ps(y + i * ldy + 16 * j, c[i][j]);
+}
+
+__attribute__((target("avx512f"))) static void tile1_512(const float *x, const float *p, int kc, float *y, int acc)
+{
+    __m512 c0 = acc ? _mm512_loadu_ps(y) : _mm512_setzero_ps(), c1 = acc ? _mm512_loadu_ps(y + 16) : _mm512_setzero_ps(),
+           c2 = acc ? _mm512_loadu_ps(y + 32) : _mm512_setzero_ps(), c3 = acc ? _mm512_loadu_ps(y + 48) : _mm512_setzero_ps();
+    for (int k = 0; k < kc; k++) {
+        const float *w = p + (int64_t)k * PANEL;
+        const __m512 sv = _mm512_set1_ps(x[k]);
+        c0 = _mm512_fmadd_ps(sv, _mm512_loadu_ps(w), c0);
+        c1 = _mm512_fmadd_ps(sv, _mm512_loadu_ps(w + 16), c1);
+        c2 = _mm512_fmadd_ps(sv, _mm512_loadu_ps(w + 32), c2);
+        c3 = _mm512_fmadd_ps(sv, _mm512_loadu_ps(w + 48), c3);
+    }
+    _mm512_storeu_ps(y, c0);
+    _mm512_storeu_ps(y + 16, c1);
+    _mm512_storeu_ps(y + 32, c2);
+    _mm512_storeu_ps(y + 48, c3);
+}
+#endif
+
 /* PanelGemm.RunPanel (PanelGemm.cs:87-135) for one 64-row panel: decode the
  * panel's K block into packed[k][64] (Pack, :144-164), then every token's
  * output is one fused chain over k ascending (Tile512x6 / Tile512x1,
@@ -280,6 +340,13 @@ static void run_panel(int type, const uint8_t *w, int rows, int cols, const floa
         }
         int acc = k0 != 0;
         int t = 0;
+#if defined(__x86_64__)
+        if (orc_get_vector_bits() == 512) {
+            for (; t + ROWBLK <= tokens; t += ROWBLK)
+                tile6_512(x + (int64_t)t * cols + k0, cols, packed, kc, y + (int64_t)t * rows + r0, rows, acc);
+            for (; t < tokens; t++) tile1_512(x + (int64_t)t * cols + k0, packed, kc, y + (int64_t)t * rows + r0, acc);
+        }
+#endif
         for (; t + ROWBLK <= tokens; t += ROWBLK) {
             float c[ROWBLK][PANEL];
             for (int i = 0; i < ROWBLK; i++)

@@ -143,6 +143,10 @@ void orc_margins(const float *verdicts, int n_options, int n_yes, int n_no, floa
 
 void orc_set_threads(int n);
 int orc_get_threads(void);
+/* PanelGemm.VectorBits (PanelGemm.cs:50-63): 512 or 256 forces a tile width,
+ * 0 picks 512 when the host has AVX-512F.  Both widths give the same bits. */
+void orc_set_vector_bits(int bits);
+int orc_get_vector_bits(void);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,8 @@ def lib():
             "orc_layout_rows": (c_int, [c_int, I, I, I, c_int, I, I, I, I, I]),
             "orc_margins": (None, [F, c_int, c_int, c_int, c_float, F, F]),
             "orc_set_threads": (None, [c_int]),
+            "orc_set_vector_bits": (None, [c_int]),
+            "orc_get_vector_bits": (c_int, []),
             "orc_get_threads": (c_int, []),
         }
         for name, (res, args) in sig.items():
@@ -109,6 +111,15 @@ def i32(a):
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(n)
+
+
+def set_vector_bits(bits: int) -> None:
+    """PanelGemm.VectorBits: 512, 256, or 0 for the host's widest (same bits either way)."""
+    lib().orc_set_vector_bits(bits)
+
+
+def vector_bits() -> int:
+    return int(lib().orc_get_vector_bits())
 
 
 def dequantize(ggml_type: int, raw: np.ndarray, count: int) -> np.ndarray:

@@ -222,3 +222,22 @@ def test_margins_and_probabilities():
     assert np.allclose(p, e / e.sum(), rtol=1e-6)
     jm, jp = jev.margins(v, 2, 2, 1.0)
     assert np.array_equal(jm, m) and np.allclose(jp, p, rtol=1e-6)
+
+
+@pytest.mark.skipif(oracle.vector_bits() != 512, reason="the host has no AVX-512F")
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+def test_panel_tile_widths_give_the_same_bits(t):
+    # PanelGemm.VectorBits (PanelGemm.cs:50-63): the 512- and 256-bit tiles run
+    # the same fused chain per output, so the oracle's CPU baseline on an
+    # AVX-512 host computes exactly what the 256-bit path computes
+    rows, cols, tokens = 128, 2304, 13  # two K blocks, a six-token remainder of 1
+    raw = jev.synth_tensor("widths", t, rows, cols)
+    x = np.random.default_rng(5).standard_normal((tokens, cols)).astype(np.float32)
+    try:
+        oracle.set_vector_bits(256)
+        narrow = oracle.matmul(t, raw, rows, cols, x, tokens)
+        oracle.set_vector_bits(512)
+        wide = oracle.matmul(t, raw, rows, cols, x, tokens)
+    finally:
+        oracle.set_vector_bits(0)
+    assert np.array_equal(narrow.view(np.uint32), wide.view(np.uint32))
