@@ -92,6 +92,10 @@ struct GemmArgs {
     int ksplit = 1;                      // store mode: K in ksplit ranges, partial z at y + z*M*ldy
     uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
     int mode = kGemmStore;
+    // Optional timing: the kernel is launched with these events stamped by its
+    // own dispatch (hipExtLaunchKernelGGL), so the elapsed time is the
+    // kernel's alone, not an event marker's on either side of it.
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
 

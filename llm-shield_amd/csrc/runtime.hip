@@ -221,19 +221,31 @@ struct ProfScope {
     jev_ctx *c;
     int cls;
     double flops, bytes;
-    hipEvent_t a = nullptr;
-    ProfScope(jev_ctx *ctx, int k, double f, double b) : c(ctx), cls(k), flops(f), bytes(b)
+    hipEvent_t a = nullptr, z = nullptr;
+    bool stamped = false;
+    // stamped: the caller's one kernel launch stamps a and z itself
+    // (hipExtLaunchKernelGGL, GemmArgs::ev_start / ev_stop), so the time is the
+    // kernel's alone; otherwise event markers bracket everything in the scope.
+    ProfScope(jev_ctx *ctx, int k, double f, double b, bool by_launch = false)
+        : c(ctx), cls(k), flops(f), bytes(b)
     {
         if (!c->profiling || c->capturing) return;
         a = next_event();
+        if (by_launch) {
+            z = next_event();
+            stamped = true;
+            return;
+        }
         (void)hipEventRecord(a, c->stream);
     }
     ~ProfScope()
     {
         if (!a) return;
-        hipEvent_t b2 = next_event();
-        (void)hipEventRecord(b2, c->stream);
-        c->prof.push_back({cls, a, b2, flops, bytes});
+        if (!stamped) {
+            z = next_event();
+            (void)hipEventRecord(z, c->stream);
+        }
+        c->prof.push_back({cls, a, z, flops, bytes});
     }
     hipEvent_t next_event()
     {
@@ -380,7 +392,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
         HIP_TRY(launch_gemv(g, c->stream));
         return JEV_OK;
     }
-    ProfScope ps(c, JEV_PROF_GEMM, 2.0 * T * nrows * K, wbytes + T * (4.0 * K + 4.0 * nrows));
+    ProfScope ps(c, JEV_PROF_GEMM, 2.0 * T * nrows * K, wbytes + T * (4.0 * K + 4.0 * nrows), true);
     GemmArgs g;
     g.M = T;
     g.K = ws[0]->cols;
@@ -391,6 +403,8 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     g.ldy = ldy;
     g.y = y;
     g.ksplit = ksplit;
+    g.ev_start = ps.a;
+    g.ev_stop = ps.z;
     HIP_TRY(launch_gemm(g, c->stream));
     return JEV_OK;
 }
@@ -888,9 +902,13 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             g.seg[1] = L.up;
             g.mode = kGemmSwiGlu;
             g.ot = c->ft.p;
-            ProfScope ps(c, JEV_PROF_GEMM, 4.0 * T * f.ffn * D,
-                         weight_bytes(L.gate) + weight_bytes(L.up) + T * (4.0 * D + 4.0 * f.ffn));
-            HIP_TRY(launch_gemm(g, s));
+            {
+                ProfScope ps(c, JEV_PROF_GEMM, 4.0 * T * f.ffn * D,
+                             weight_bytes(L.gate) + weight_bytes(L.up) + T * (4.0 * D + 4.0 * f.ffn), true);
+                g.ev_start = ps.a;
+                g.ev_stop = ps.z;
+                HIP_TRY(launch_gemm(g, s));
+            }
             if (L.down.type == kQ5_1) HIP_TRY(launch_block_sums(c->ft.p, T, f.ffn, c->xsum.p, s));
         }
         {
@@ -968,7 +986,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         g.seg[0] = tab;
         g.ldy = tab.rows;
         g.y = dout;
-        ProfScope ps(c, JEV_PROF_GEMM, 2.0 * p.n_out * tab.rows * D, weight_bytes(tab) + p.n_out * 4.0 * (D + tab.rows));
+        ProfScope ps(c, JEV_PROF_GEMM, 2.0 * p.n_out * tab.rows * D, weight_bytes(tab) + p.n_out * 4.0 * (D + tab.rows),
+                     true);
+        g.ev_start = ps.a;
+        g.ev_stop = ps.z;
         HIP_TRY(launch_gemm(g, s));
     }
     return JEV_OK;
