@@ -2,12 +2,26 @@
 // of the field-split weight layout (see QWeight in jev_internal.h).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "jev_internal.h"
 
 namespace jev {
+
+// Kernel launch with optional timing events (a profiled pass): given both,
+// the dispatch itself stamps them (hipExtLaunchKernelGGL), so their elapsed
+// time is this kernel's alone rather than a marker's on either side of it.
+template <typename Kernel, typename... Args>
+inline void launch_stamped(hipEvent_t e0, hipEvent_t e1, Kernel k, dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                           Args... args)
+{
+    if (e0 && e1)
+        hipExtLaunchKernelGGL(k, grid, block, lds, s, e0, e1, 0, args...);
+    else
+        hipLaunchKernelGGL(k, grid, block, lds, s, args...);
+}
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -92,10 +92,7 @@ struct GemmArgs {
     int ksplit = 1;                      // store mode: K in ksplit ranges, partial z at y + z*M*ldy
     uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
     int mode = kGemmStore;
-    // Optional timing: the kernel is launched with these events stamped by its
-    // own dispatch (hipExtLaunchKernelGGL), so the elapsed time is the
-    // kernel's alone, not an event marker's on either side of it.
-    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
 
@@ -173,6 +170,7 @@ struct GemvArgs {
     // attn.part set: x is unused; the input is the decode attention output,
     // its chunks merged in ascending order while staging
     DecodeChunks attn;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 // GEMV shape rules, functions of the weight shape only.  Many rows: each wave
@@ -250,6 +248,7 @@ struct AttnArgs {
     int cap = 0;
     float scale = 0.f;
     uint16_t *ot = nullptr; // context pair, operand-tile layout, K = qdim
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 
@@ -273,6 +272,7 @@ struct DecodeAttnArgs {
     // them -- instead of in rope_store_kernel; `q` is then unused.
     int rope_fused = 0;
     RopeArgs rope;
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
 

@@ -373,11 +373,11 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
     // fewer workgroups than compute units: the output dims split over two or four
     const long wgs = (long)grid.x * grid.y;
     if (wgs <= 64)
-        hipLaunchKernelGGL(attn_tree_kernel<4>, dim3(grid.x, grid.y, 4), dim3(256), 0, s, a);
+        launch_stamped(a.ev_start, a.ev_stop, attn_tree_kernel<4>, dim3(grid.x, grid.y, 4), dim3(256), 0, s, a);
     else if (wgs < 256)
-        hipLaunchKernelGGL(attn_tree_kernel<2>, dim3(grid.x, grid.y, 2), dim3(256), 0, s, a);
+        launch_stamped(a.ev_start, a.ev_stop, attn_tree_kernel<2>, dim3(grid.x, grid.y, 2), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(attn_tree_kernel<1>, grid, dim3(256), 0, s, a);
+        launch_stamped(a.ev_start, a.ev_stop, attn_tree_kernel<1>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -611,7 +611,8 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
                          !a.rope.k_in || !a.rope.v_in || !a.rope.kc || !a.rope.vc || !a.rope.kp || !a.rope.vp ||
                          !a.rope.freqs || a.rope.kc != a.kc || a.rope.vc != a.vc))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s, a);
+    launch_stamped(a.ev_start, a.ev_stop, attn_decode_kernel, dim3(a.T, a.n_heads / a.group, a.max_chunks), dim3(256), 0, s,
+                   a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return hipGetLastError();

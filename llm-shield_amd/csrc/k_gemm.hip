@@ -34,7 +34,6 @@
 // (144 B) so 16-byte fragment reads of 8 lanes hit distinct banks.
 #include "jev_dev.h"
 
-#include <hip/hip_ext.h>
 #include <type_traits>
 
 namespace jev {
@@ -961,16 +960,6 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
     }
 }
 
-// Launch, with the caller's timing events stamped by the dispatch when given.
-template <typename Kernel, typename... Args>
-static void launch_timed(const GemmArgs &a, Kernel k, dim3 grid, hipStream_t s, Args... args)
-{
-    if (a.ev_start && a.ev_stop)
-        hipExtLaunchKernelGGL(k, grid, dim3(256), 0, s, a.ev_start, a.ev_stop, 0, args...);
-    else
-        hipLaunchKernelGGL(k, grid, dim3(256), 0, s, args...);
-}
-
 template <int TYPE, int MODE, int U, int CH>
 static hipError_t launch_skinny(const GemmArgs &a, hipStream_t s)
 {
@@ -984,7 +973,8 @@ static hipError_t launch_skinny(const GemmArgs &a, hipStream_t s)
         ngroups = (ntot + 15) / 16;
     }
     const int nq = (ngroups + 3) / 4;
-    launch_timed(a, gemm_skinny_kernel<TYPE, MODE, U, CH>, dim3(nq * a.ksplit), s, a, ngroups, nq);
+    launch_stamped(a.ev_start, a.ev_stop, gemm_skinny_kernel<TYPE, MODE, U, CH>, dim3(nq * a.ksplit), dim3(256), 0, s, a,
+                   ngroups, nq);
     return hipGetLastError();
 }
 
@@ -1007,7 +997,8 @@ static hipError_t launch_bd(const GemmArgs &a, hipStream_t s, int gm_cap = 8)
     int gm = mt <= gm_cap ? mt : gm_cap;
     int tiles = mt * ncols;
     int grid = ((tiles + 7) & ~7) * a.ksplit;
-    launch_timed(a, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC>, dim3(grid), s, a, mt, ncols, gm);
+    launch_stamped(a.ev_start, a.ev_stop, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC>, dim3(grid), dim3(256), 0, s, a, mt,
+                   ncols, gm);
     return hipGetLastError();
 }
 
@@ -1027,7 +1018,8 @@ static hipError_t launch_cfg(const GemmArgs &a, hipStream_t s)
     int gm = mt <= 8 ? mt : 8;
     int tiles = mt * ncols;
     int grid = ((tiles + 7) & ~7) * a.ksplit;
-    launch_timed(a, gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD, KS, OCC>, dim3(grid), s, a, mt, ncols, gm);
+    launch_stamped(a.ev_start, a.ev_stop, gemm_q_kernel<TYPE, MODE, WM, WN, TM, TN, PD, KS, OCC>, dim3(grid), dim3(256), 0,
+                   s, a, mt, ncols, gm);
     return hipGetLastError();
 }
 

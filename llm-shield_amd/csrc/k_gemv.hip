@@ -351,9 +351,11 @@ static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
     const int ntw = nbz / 2, per = WR == 4 ? ntw : (ntw + 3) / 4;
     const int pad4 = (per + 3) / 4 * 4 - per, pad2 = (per + 1) / 2 * 2 - per;
     if (pad2 < pad4)
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 2, ATTN>), grid, dim3(256), lds, s, a, rows, nbz);
+        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 2, ATTN>, grid, dim3(256), (uint32_t)lds, s, a,
+                       rows, nbz);
     else
-        hipLaunchKernelGGL((gemv_q_kernel<TYPE, WR, SWIGLU, 4, ATTN>), grid, dim3(256), lds, s, a, rows, nbz);
+        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 4, ATTN>, grid, dim3(256), (uint32_t)lds, s, a,
+                       rows, nbz);
     return hipGetLastError();
 }
 

@@ -388,7 +388,9 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
         g.ksplit = ksplit;
         g.x_up = x_up;
         if (attn) g.attn = *attn;
-        ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows));
+        ProfScope ps(c, JEV_PROF_GEMV, 2.0 * nrows * K, wbytes + 4.0 * (K + nrows), true);
+        g.ev_start = ps.a;
+        g.ev_stop = ps.z;
         HIP_TRY(launch_gemv(g, c->stream));
         return JEV_OK;
     }
@@ -829,7 +831,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             dchunks.start = da.start;
             dchunks.start_dev = da.start_dev;
             ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
-                         8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs);
+                         8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs, true);
+            da.ev_start = ps.a;
+            da.ev_stop = ps.z;
             HIP_TRY(launch_attn_decode(da, s));
             CAP_TRY(cap_chunks(c, cap, layer_tap(l, "attn_weighted"), c->part.p, p.max_chunks,
                                (p.start + 1 + kDecodeKeys - 1) / kDecodeKeys));
@@ -848,7 +852,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             aa.ot = c->xt.p;
             {
                 ProfScope ps(c, JEV_PROF_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
-                             8.0 * f.head_dim * f.n_kv_heads * p.kv_rows + 8.0 * T * qdim);
+                             8.0 * f.head_dim * f.n_kv_heads * p.kv_rows + 8.0 * T * qdim, true);
+                aa.ev_start = ps.a;
+                aa.ev_stop = ps.z;
                 HIP_TRY(launch_attn_tree(aa, s));
             }
             CAP_TRY(cap_pair(c, cap, layer_tap(l, "attn_weighted"), c->xt.p, T, qdim));
@@ -889,7 +895,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             g.seg[1] = L.up;
             g.y = c->f32.p;
             g.swiglu = 1;
-            ProfScope ps(c, JEV_PROF_GEMV, 4.0 * f.ffn * D, weight_bytes(L.gate) + weight_bytes(L.up) + 4.0 * (D + f.ffn));
+            ProfScope ps(c, JEV_PROF_GEMV, 4.0 * f.ffn * D, weight_bytes(L.gate) + weight_bytes(L.up) + 4.0 * (D + f.ffn),
+                         true);
+            g.ev_start = ps.a;
+            g.ev_stop = ps.z;
             HIP_TRY(launch_gemv(g, s));
         } else {
             GemmArgs g;
@@ -969,7 +978,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         g.seg[0] = tab;
         g.y = dout;
         {
-            ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows));
+            ProfScope ps(c, JEV_PROF_GEMV, 2.0 * tab.rows * D, weight_bytes(tab) + 4.0 * (D + tab.rows), true);
+            g.ev_start = ps.a;
+            g.ev_stop = ps.z;
             HIP_TRY(launch_gemv(g, s));
         }
         CAP_TRY(cap_add(c, cap, "logits", dout, 1, tab.rows));
