@@ -254,6 +254,14 @@ def test_errors_match_reference_exceptions(model):
     with pytest.raises(jev.ArgumentError):
         m.kv_snapshot(5)
     assert m.cached_token_count == 0
+    # RopeAndCacheTests.RestoreRejectsAMissizedSnapshot / SnapshotRejectsMoreThanIsCached
+    m.forward([1, 2])
+    snap = m.kv_snapshot(2)
+    with pytest.raises(jev.ArgumentError):
+        m.kv_restore(snap, 3)
+    with pytest.raises(jev.ArgumentError):
+        m.kv_snapshot(3)
+    assert m.cached_token_count == 2
 
 
 def test_cancel_aimed_at_no_call_does_not_reach_the_next_one(model):
