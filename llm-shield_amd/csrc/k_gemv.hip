@@ -228,14 +228,19 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
             v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
             v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
             if (a.x_up > 0) {
-                // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g)
+                // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g).  Every
+                // workgroup of the down projection forms the inputs of its K
+                // range (192 row groups each redo them), so the sigmoid is the
+                // hardware exp2 and reciprocal (a few ulp, as TensorPrimitives'
+                // vectorised Sigmoid is not libm either) rather than the
+                // library's exact expf and IEEE division.
                 const float4 u0 = xp[a.x_up / 4], u1 = xp[a.x_up / 4 + 1];
                 const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const float gu = v[j] * u[j];
-                    const float e = expf(-v[j]);
-                    const float sg = 1.0f / (1.0f + e);
+                    const float e = __builtin_amdgcn_exp2f(-v[j] * 1.44269504088896340736f);
+                    const float sg = __builtin_amdgcn_rcpf(1.0f + e);
                     v[j] = sg * gu;
                 }
             }
