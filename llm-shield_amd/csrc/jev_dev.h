@@ -130,13 +130,15 @@ __device__ __forceinline__ float warp_max(float v)
 }
 
 // Kernels.RmsNorm's statistics (Kernels.cs:25-60) for one row of D floats in
-// a workgroup of 256 threads: thread t owns the float4 groups g = t + 256 i
+// a workgroup of NT threads: thread t owns the float4 groups g = t + NT i
 // (i < NI), x[i] = h + the sum of the `nadd` K-split partials taken in split
 // order (Kernels.Add first), squares summed per thread in group order, then by
-// a fixed butterfly per wave and the four wave sums in order.  Returns
-// 1 / sqrt(sum / D + eps).  `wsum` is 4 floats of LDS.  Groups a thread does
-// not own (g >= D / 4) load a clamped neighbour and are left out of the sum.
-template <int NI, int NP>
+// a fixed butterfly per wave and the NT / 64 wave sums in order.  Returns
+// 1 / sqrt(sum / D + eps).  `wsum` is NT / 64 floats of LDS.  Groups a thread
+// does not own (g >= D / 4) load a clamped neighbour and are left out of the
+// sum.  The order is a function of NT: every caller of one width gets the
+// same bits.
+template <int NI, int NP, int NT = 256>
 __device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *add4, int nadd, size_t pstride, int D,
                                                float eps, float4 (&x)[NI], float *wsum)
 {
@@ -144,8 +146,8 @@ __device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *a
     float4 p[NP][NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-        if (256 * i >= ng) break;
-        x[i] = h4[min(tid + 256 * i, ng - 1)];
+        if (NT * i >= ng) break;
+        x[i] = h4[min(tid + NT * i, ng - 1)];
     }
     if (add4) {
 #pragma unroll
@@ -153,15 +155,15 @@ __device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *a
             if (z >= nadd) break;
 #pragma unroll
             for (int i = 0; i < NI; i++) {
-                if (256 * i >= ng) break;
-                p[z][i] = add4[z * pstride + min(tid + 256 * i, ng - 1)];
+                if (NT * i >= ng) break;
+                p[z][i] = add4[z * pstride + min(tid + NT * i, ng - 1)];
             }
         }
     }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-        if (256 * i >= ng) break;
+        if (NT * i >= ng) break;
         float4 v = x[i];
         if (add4) {
             float4 s4 = p[0][i];
@@ -179,7 +181,7 @@ __device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *a
             v.w = v.w + s4.w;
         }
         x[i] = v;
-        if (tid + 256 * i < ng) {
+        if (tid + NT * i < ng) {
             float q0 = v.x * v.x, q1 = v.y * v.y, q2 = v.z * v.z, q3 = v.w * v.w;
             ss = ss + q0;
             ss = ss + q1;
@@ -190,7 +192,9 @@ __device__ __forceinline__ float row_rms_scale(const float4 *h4, const float4 *a
     ss = warp_sum(ss);
     if ((tid & 63) == 0) wsum[tid >> 6] = ss;
     __syncthreads();
-    const float sum = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    float sum = wsum[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) sum = sum + wsum[w];
     return 1.0f / sqrtf(sum / (float)D + eps);
 }
 

@@ -220,8 +220,9 @@ __global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int 
                     }
                 }
             }
+            const float inv = 1.0f / L; // one division, eight products
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = v[e] / L;
+            for (int e = 0; e < 8; e++) v[e] = v[e] * inv;
         } else if (i < nbw * 4) {
             const float4 *xp = (const float4 *)(a.x + (size_t)kb0 * 32 + 8 * i);
             const float4 v0 = xp[0], v1 = xp[1];

@@ -102,11 +102,11 @@ __device__ __forceinline__ int norm_row(int L, int T)
     return (j & 15) + 16 * ((j >> 4) * 8 + x);
 }
 
-template <int NI>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
+template <int NI, int NT = 256>
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(NormArgs a)
 {
     constexpr int kNormIters = NI;
-    __shared__ float wsum[4];
+    __shared__ float wsum[NT / 64];
     const int t = norm_row(blockIdx.x, a.T), tid = threadIdx.x;
     const int row = a.rows ? a.rows[t] : t;
     const int ng = a.D >> 2, nblk = a.D >> 5;
@@ -116,21 +116,21 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a)
     const float4 *w4 = (const float4 *)a.w;
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
-        if (256 * i >= ng) break;
-        wv[i] = w4[min(tid + 256 * i, ng - 1)]; // clamped: out-of-row lanes load and drop
+        if (NT * i >= ng) break;
+        wv[i] = w4[min(tid + NT * i, ng - 1)]; // clamped: out-of-row lanes load and drop
     }
-    const float scale = row_rms_scale<kNormIters, kNormParts>(h4, add4, a.nadd, a.add_stride >> 2, a.D, a.eps, x, wsum);
+    const float scale = row_rms_scale<kNormIters, kNormParts, NT>(h4, add4, a.nadd, a.add_stride >> 2, a.D, a.eps, x, wsum);
     if (add4 && a.store_h) {
 #pragma unroll
         for (int i = 0; i < kNormIters; i++) {
-            if (256 * i >= ng) break;
-            if (tid + 256 * i < ng) h4[tid + 256 * i] = x[i];
+            if (NT * i >= ng) break;
+            if (tid + NT * i < ng) h4[tid + NT * i] = x[i];
         }
     }
 #pragma unroll
     for (int i = 0; i < kNormIters; i++) {
-        if (256 * i >= ng) break;
-        const int g = tid + 256 * i;
+        if (NT * i >= ng) break;
+        const int g = tid + NT * i;
         const bool own = g < ng;
         const float4 w = wv[i];
         float y[4] = {(x[i].x * scale) * w.x, (x[i].y * scale) * w.y, (x[i].z * scale) * w.z, (x[i].w * scale) * w.w};
@@ -166,6 +166,17 @@ hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
     if (a.T <= 0) return hipSuccess;
     if (a.D % 32 != 0 || a.D > 4 * 256 * kNormIters || a.nadd < 1 || a.nadd > kNormParts) return hipErrorInvalidValue;
     if (a.xsum && !a.ot) return hipErrorInvalidValue;
+    // The per-layer norms of a one-token pass (one row, no row list, no
+    // operand tiles: the one-token GEMV reads fp32): 1024 threads, a quarter
+    // of the serial work per thread on the latency path.  Their reduction
+    // order is their own; a single token already takes the one-token GEMV
+    // rather than the batched arithmetic.  The head norm (a row list) keeps
+    // one order for any number of outputs, so a tree's verdicts still equal
+    // its branches run alone bit for bit.
+    if (a.T == 1 && !a.rows && !a.ot && a.D <= 4 * 1024) {
+        hipLaunchKernelGGL((rmsnorm_kernel<1, 1024>), dim3(1), dim3(1024), 0, s, a);
+        return hipGetLastError();
+    }
     switch ((a.D / 4 + 255) / 256) {
     case 1: hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(a.T), dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(a.T), dim3(256), 0, s, a); break;

@@ -673,7 +673,8 @@ int cap_chunks(jev_ctx *c, Capture *cap, std::string name, const float *part, in
             for (int d = 0; d < hd; d++) o[d] = fmaf(pc[2 + d], fc, o[d] * fo);
             M = Mn;
         }
-        for (int d = 0; d < hd; d++) o[d] = o[d] / L;
+        const float inv = 1.0f / L; // as the O projection's staging normalises
+        for (int d = 0; d < hd; d++) o[d] = o[d] * inv;
     }
     cap->taps.push_back(std::move(t));
     return JEV_OK;
