@@ -119,7 +119,7 @@ struct TileLoader {
 // carries few clamped reloads.
 // ATTN: the input is the decode attention output (GemvArgs::attn).
 template <int TYPE, int WR, bool SWIGLU, int DEPTH, bool ATTN>
-__global__ __launch_bounds__(256) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
+__global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int NW = SWIGLU ? 2 : 1; // weights per row (gate and up)
