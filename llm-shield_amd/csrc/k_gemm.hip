@@ -605,8 +605,25 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // Large tiles: the scale FMAs of a tile trail its MFMA pair by two pairs
+    // (the result is ready by then, so the vector ALU works beside the matrix
+    // core instead of waiting on it; 2-4 % at 4528 rows, nothing at 256).
+    // Each accumulator still takes its blocks' FMAs in block order, so the
+    // arithmetic is that of the plain order.
     auto compute = [&](int st, int buf, const BChunk (&br)[TN]) __attribute__((always_inline)) {
         const bool second = 2 * st + 1 < nb;
+        constexpr int LAG = TM * TN >= 16 ? 2 : 0, NQ = 2 * TM * TN;
+        floatx4 pq[LAG > 0 ? LAG : 1], xq[LAG > 0 ? LAG : 1];
+        float dq[LAG > 0 ? LAG : 1], mq[LAG > 0 ? LAG : 1];
+        auto apply = [&](int t) __attribute__((always_inline)) {
+            const int mt_ = (t / TN) % TM, nt_ = t % TN, k = LAG > 0 ? t % LAG : 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = fmaf(dq[k], pq[k][r], acc[mt_][nt_][r]);
+                if (TYPE == kQ5_1) v = fmaf(mq[k], xq[k][r], v);
+                acc[mt_][nt_][r] = v;
+            }
+        };
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
             // an odd block count's missing second block adds 0 * p (p is finite)
@@ -632,14 +649,31 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
                 for (int n = 0; n < TN; n++) {
                     floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[n], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[n], p, 0, 0, 0);
+                    if constexpr (LAG == 0) {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        float v = fmaf(dv[n], p[r], acc[mi][n][r]);
-                        if (TYPE == kQ5_1) v = fmaf(mv[n], xs4[r], v);
-                        acc[mi][n][r] = v;
+                        for (int r = 0; r < 4; r++) {
+                            float v = fmaf(dv[n], p[r], acc[mi][n][r]);
+                            if (TYPE == kQ5_1) v = fmaf(mv[n], xs4[r], v);
+                            acc[mi][n][r] = v;
+                        }
+                    } else {
+                        const int q = (bb * TM + mi) * TN + n;
+                        if (q >= LAG) apply(q - LAG);
+                        pq[q % LAG] = p;
+                        dq[q % LAG] = dv[n];
+                        if (TYPE == kQ5_1) {
+                            xq[q % LAG] = xs4;
+                            mq[q % LAG] = mv[n];
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); // the pair's MFMAs
+                        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0); // then vector work
                     }
                 }
             }
+        }
+        if constexpr (LAG > 0) {
+#pragma unroll
+            for (int t = NQ - LAG; t < NQ; t++) apply(t);
         }
     };
 
