@@ -118,7 +118,8 @@ struct TileLoader {
 // pairs) per pipeline stage, chosen per shape so that a wave's last stage
 // carries few clamped reloads.
 // ATTN: the input is the decode attention output (GemvArgs::attn).
-template <int TYPE, int WR, bool SWIGLU, int DEPTH, bool ATTN>
+// XUP: the input is the SwiGLU of a gate and an up row (GemvArgs::x_up).
+template <int TYPE, int WR, bool SWIGLU, int DEPTH, bool ATTN, bool XUP>
 __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, int nbz)
 {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -160,10 +161,31 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
             for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp);
         }
     };
-    // the first stage's weights are in flight while x is staged
+    // x of the first kPre groups of 256 is loaded before the first stage's
+    // weights, which are in flight while x is staged: the staging then waits
+    // on x alone (the vector-memory counter retires loads in order, so a load
+    // issued after the weights would wait for them too)
+    constexpr int kPre = 2;
     const int nst = (ntiles + DEPTH - 1) / DEPTH;
     RawTile r0[NW][DEPTH], r1[NW][DEPTH];
-    if (nst > 0) load_stage(0, r0);
+    // (clamped, unconditional loads: the buffer loads of a wave without
+    // tiles stay inside the weight and feed nothing; branches here would make
+    // the compiler drain every outstanding load where they join)
+    float4 px[kPre][2], pu[kPre][2];
+    if (!ATTN) {
+#pragma unroll
+        for (int it = 0; it < kPre; it++) {
+            const int i = min(256 * it + tid, nbw * 4 - 1);
+            const float4 *xp = (const float4 *)(a.x + (size_t)kb0 * 32 + 8 * i);
+            px[it][0] = xp[0];
+            px[it][1] = xp[1];
+            if (XUP) {
+                pu[it][0] = xp[a.x_up / 4];
+                pu[it][1] = xp[a.x_up / 4 + 1];
+            }
+        }
+    }
+    load_stage(0, r0);
 
     // ---- x pair of the workgroup's K range (zero past K), a zero slot, Q5_1 block sums
     uint16_t *xh = (uint16_t *)smem, *xl = xh + nbz * 32, *zero = xl + nbz * 32;
@@ -183,7 +205,8 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
         nch = min((limit + kDecodeKeys - 1) / kDecodeKeys, d.max_chunks);
     }
     // thread -> 8 consecutive elements; a block's four groups are neighbouring lanes
-    for (int i0 = 0; i0 < 2 * ntw * 4; i0 += 256) {
+    auto stage_group = [&](int i0, auto prec) __attribute__((always_inline)) {
+        constexpr int PRE = decltype(prec)::value; // prefetched group index, or -1
         const int i = i0 + tid;
         float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (ATTN && i < nbw * 4) {
@@ -223,19 +246,24 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
             const float inv = 1.0f / L; // one division, eight products
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = v[e] * inv;
-        } else if (i < nbw * 4) {
+        } else if (PRE >= 0 || i < nbw * 4) {
+            // a prefetched group selects rather than branches (its lanes past
+            // the range hold clamped copies and stage zeros)
+            const bool valid = i < nbw * 4;
             const float4 *xp = (const float4 *)(a.x + (size_t)kb0 * 32 + 8 * i);
-            const float4 v0 = xp[0], v1 = xp[1];
+            const float4 v0 = PRE >= 0 ? px[PRE < 0 ? 0 : PRE][0] : xp[0];
+            const float4 v1 = PRE >= 0 ? px[PRE < 0 ? 0 : PRE][1] : xp[1];
             v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
             v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
-            if (a.x_up > 0) {
+            if (XUP) {
                 // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g).  Every
                 // workgroup of the down projection forms the inputs of its K
                 // range (192 row groups each redo them), so the sigmoid is the
                 // hardware exp2 and reciprocal (a few ulp, as TensorPrimitives'
                 // vectorised Sigmoid is not libm either) rather than the
                 // library's exact expf and IEEE division.
-                const float4 u0 = xp[a.x_up / 4], u1 = xp[a.x_up / 4 + 1];
+                const float4 u0 = PRE >= 0 ? pu[PRE < 0 ? 0 : PRE][0] : xp[a.x_up / 4];
+                const float4 u1 = PRE >= 0 ? pu[PRE < 0 ? 0 : PRE][1] : xp[a.x_up / 4 + 1];
                 const float u[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
@@ -245,6 +273,8 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
                     v[j] = sg * gu;
                 }
             }
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = valid ? v[j] : 0.f;
         }
         uint32_t hw[4], lw[4];
         float bs = 0.f;
@@ -266,7 +296,11 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
             bs = bs + __shfl_xor(bs, 2, 64);
             if (i < 2 * ntw * 4 && (i & 3) == 0) xsum[i >> 2] = bs;
         }
-    }
+    };
+    // the prefetched groups in straight-line code, any further ones in a loop
+    stage_group(0, std::integral_constant<int, ATTN ? -1 : 0>{});
+    if (256 < 2 * ntw * 4) stage_group(256, std::integral_constant<int, ATTN ? -1 : 1>{});
+    for (int i0 = 256 * kPre; i0 < 2 * ntw * 4; i0 += 256) stage_group(i0, std::integral_constant<int, -1>{});
     if (tid < 8) zero[tid] = 0;
     __syncthreads();
 
@@ -344,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
     }
 }
 
-template <int TYPE, int WR, bool SWIGLU, bool ATTN = false>
+template <int TYPE, int WR, bool SWIGLU, bool ATTN = false, bool XUP = false>
 static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
 {
     const int nb = a.K >> 5;
@@ -357,10 +391,10 @@ static hipError_t launch_gemv_cfg(const GemvArgs &a, int rows, hipStream_t s)
     const int ntw = nbz / 2, per = WR == 4 ? ntw : (ntw + 3) / 4;
     const int pad4 = (per + 3) / 4 * 4 - per, pad2 = (per + 1) / 2 * 2 - per;
     if (pad2 < pad4)
-        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 2, ATTN>, grid, dim3(256), (uint32_t)lds, s, a,
+        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 2, ATTN, XUP>, grid, dim3(256), (uint32_t)lds, s, a,
                        rows, nbz);
     else
-        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 4, ATTN>, grid, dim3(256), (uint32_t)lds, s, a,
+        launch_stamped(a.ev_start, a.ev_stop, gemv_q_kernel<TYPE, WR, SWIGLU, 4, ATTN, XUP>, grid, dim3(256), (uint32_t)lds, s, a,
                        rows, nbz);
     return hipGetLastError();
 }
@@ -374,6 +408,10 @@ static hipError_t launch_gemv_typed(const GemvArgs &a, hipStream_t s)
     if (a.attn.part) {
         if (gemv_rows_mode(rows)) return launch_gemv_cfg<TYPE, 4, false, true>(a, rows, s);
         return launch_gemv_cfg<TYPE, 1, false, true>(a, rows, s);
+    }
+    if (a.x_up > 0) {
+        if (gemv_rows_mode(rows)) return hipErrorInvalidValue; // the SwiGLU input is a narrow projection's
+        return launch_gemv_cfg<TYPE, 1, false, false, true>(a, rows, s);
     }
     if (gemv_rows_mode(rows)) return launch_gemv_cfg<TYPE, 4, false>(a, rows, s);
     return launch_gemv_cfg<TYPE, 1, false>(a, rows, s);
