@@ -416,12 +416,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     const int nchunks = (limit + kDecKeys - 1) / kDecKeys;
     if (c >= nchunks) return; // this token sees fewer keys
 
-    // ---- the chunk's K and V rows (logical key -> cache slot), all loads in
-    // flight before the first store, then this wave's first query head
+    // ---- loads, all in flight before the first use and issued in the order
+    // they are needed (the vector-memory counter retires loads in order, so
+    // waiting on one waits on every older one): the RoPE frequency, the first
+    // query head's projection partials, the chunk's K and V rows (logical key
+    // -> cache slot), then the new key's and value's partials.  The hoisted
+    // loads are unconditional with in-range addresses (the projection and
+    // frequency buffers are set whether or not RoPE is fused here) and feed
+    // nothing where unused.
+    const RopeArgs &r = a.rope;
+    const size_t zs = r.in_stride;
+    constexpr int kHoist = 2; // projection K-split partials loaded up front
+    const bool hoisted = r.nin <= kHoist;
+    const int head0 = kvh * a.group + min(wave, a.group - 1);
+    const float fr = r.freqs[min(tid, max(r.half, 1) - 1)];
+    __builtin_amdgcn_sched_barrier(0); // keep the issue order
+    float qx[kHoist][2];
+#pragma unroll
+    for (int z = 0; z < kHoist; z++) {
+        const float *qi = r.q_in + min(z, r.nin - 1) * zs + (size_t)t * r.ld_in + head0 * 128;
+        qx[z][0] = qi[lane];
+        qx[z][1] = qi[lane + 64];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const float *kbase = a.kc + (size_t)kvh * a.cap * 128;
     const float *vbase = a.vc + (size_t)kvh * a.cap * 128;
     const int nk = min(kDecKeys, limit - c * kDecKeys);
-    // issued before the RoPE work below, which they do not depend on
     float4 kv[kDecLoads], vv[kDecLoads];
 #pragma unroll
     for (int i = 0; i < kDecLoads; i++) {
@@ -432,18 +452,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         kv[i] = *(const float4 *)(kbase + (size_t)p * 128 + 4 * d4);
         vv[i] = *(const float4 *)(vbase + (size_t)p * 128 + 4 * d4);
     }
+    // the new key's and value's column 4 (tid % 32) .. + 3 (every thread loads
+    // one; the threads holding the new key's row use theirs)
+    float4 kxz[kHoist], vxz[kHoist];
+#pragma unroll
+    for (int z = 0; z < kHoist; z++) {
+        const size_t off = min(z, r.nin - 1) * zs + (size_t)t * r.ld_in + kvh * 128 + 4 * (tid & 31);
+        kxz[z] = *(const float4 *)(r.k_in + off);
+        vxz[z] = *(const float4 *)(r.v_in + off);
+    }
     // Fused RoPE + KV store (Rope.Apply, Rope.cs:112-135; ApplyPositionScale,
     // MinistralModel.cs:676-682; StoreKeys / StoreValues :649-669), the same
     // operations in the same order as rope_store_kernel: the projection's
     // K-split partials summed in split order, pairs (2i, 2i + 1) rotated by
     // cos / sin(pos * freq_i) * mscale with separate products, q scaled.
-    const RopeArgs &r = a.rope;
     const int pos = a.rope_fused ? (r.pos ? r.pos[t] : start + t) : 0;
     float qscale = 1.f;
     bool qscaled = false;
     if (a.rope_fused) {
         if (tid < r.half) {
-            const float theta = (float)pos * r.freqs[tid];
+            const float theta = (float)pos * fr;
             cs[tid] = cosf(theta) * r.mscale;
             sn[tid] = sinf(theta) * r.mscale;
         }
@@ -456,15 +484,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         }
         __syncthreads();
     }
-    const size_t zs = r.in_stride;
     // rotated q of one head: this lane holds dims `lane` and `lane + 64`; the
-    // pair partner of dim d is d ^ 1, held by lane ^ 1
-    auto rope_q = [&](int head, float &o0, float &o1) __attribute__((always_inline)) {
+    // pair partner of dim d is d ^ 1, held by lane ^ 1.  first: the wave's
+    // first head, whose partials were loaded up front.
+    auto rope_q = [&](int head, float &o0, float &o1, bool first) __attribute__((always_inline)) {
         const float *qi = r.q_in + (size_t)t * r.ld_in + head * 128;
-        float x[2] = {qi[lane], qi[lane + 64]};
-        for (int z = 1; z < r.nin; z++) {
-            x[0] = x[0] + qi[z * zs + lane];
-            x[1] = x[1] + qi[z * zs + lane + 64];
+        float x[2];
+        if (first && hoisted) {
+            x[0] = qx[0][0];
+            x[1] = qx[0][1];
+#pragma unroll
+            for (int z = 1; z < kHoist; z++) {
+                if (z >= r.nin) break;
+                x[0] = x[0] + qx[z][0];
+                x[1] = x[1] + qx[z][1];
+            }
+        } else {
+            x[0] = qi[lane];
+            x[1] = qi[lane + 64];
+            for (int z = 1; z < r.nin; z++) {
+                x[0] = x[0] + qi[z * zs + lane];
+                x[1] = x[1] + qi[z * zs + lane + 64];
+            }
         }
         float o[2];
 #pragma unroll
@@ -486,7 +527,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     };
     float q0, q1;
     if (a.rope_fused) {
-        rope_q(kvh * a.group + min(wave, a.group - 1), q0, q1);
+        rope_q(head0, q0, q1, true);
     } else {
         const float *q = a.q + (size_t)t * qdim + (kvh * a.group + min(wave, a.group - 1)) * 128;
         q0 = q[lane];
@@ -505,11 +546,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
             if (own_chunk && key == nk - 1) {
                 // the new key and value: partials summed, k rotated, stored
                 const size_t off = (size_t)t * r.ld_in + kvh * 128 + 4 * d4;
-                float4 kx = *(const float4 *)(r.k_in + off), vx = *(const float4 *)(r.v_in + off);
-                for (int z = 1; z < r.nin; z++) {
-                    const float4 ku = *(const float4 *)(r.k_in + z * zs + off), vu = *(const float4 *)(r.v_in + z * zs + off);
-                    kx = make_float4(kx.x + ku.x, kx.y + ku.y, kx.z + ku.z, kx.w + ku.w);
-                    vx = make_float4(vx.x + vu.x, vx.y + vu.y, vx.z + vu.z, vx.w + vu.w);
+                float4 kx, vx;
+                if (hoisted) {
+                    // d4 == tid % 32: this thread's up-front loads
+                    kx = kxz[0];
+                    vx = vxz[0];
+#pragma unroll
+                    for (int z = 1; z < kHoist; z++) {
+                        if (z >= r.nin) break;
+                        const float4 ku = kxz[z], vu = vxz[z];
+                        kx = make_float4(kx.x + ku.x, kx.y + ku.y, kx.z + ku.z, kx.w + ku.w);
+                        vx = make_float4(vx.x + vu.x, vx.y + vu.y, vx.z + vu.z, vx.w + vu.w);
+                    }
+                } else {
+                    kx = *(const float4 *)(r.k_in + off);
+                    vx = *(const float4 *)(r.v_in + off);
+                    for (int z = 1; z < r.nin; z++) {
+                        const float4 ku = *(const float4 *)(r.k_in + z * zs + off), vu = *(const float4 *)(r.v_in + z * zs + off);
+                        kx = make_float4(kx.x + ku.x, kx.y + ku.y, kx.z + ku.z, kx.w + ku.w);
+                        vx = make_float4(vx.x + vu.x, vx.y + vu.y, vx.z + vu.z, vx.w + vu.w);
+                    }
                 }
                 float kr[4] = {kx.x, kx.y, kx.z, kx.w};
 #pragma unroll
@@ -551,7 +607,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
         __syncthreads(); // K/V staged; the previous head's qs/ps consumed
         if (h0 > 0) {
             if (a.rope_fused) {
-                rope_q(head, q0, q1);
+                rope_q(head, q0, q1, false);
             } else {
                 const float *q = a.q + (size_t)t * qdim + head * 128;
                 q0 = q[lane];
