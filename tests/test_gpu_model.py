@@ -303,9 +303,17 @@ def test_cancel_in_flight_leaves_the_cache_and_the_next_call_intact(model):
     tokens = jev.random_tokens(4000, 2048, 23)
     want = fresh(model).forward(tokens[:500])
     m = fresh(model)
-    m.prefill(tokens[:100])
-    with pytest.raises(jev.CancelledError):
-        cancel_while_running(m, lambda: m.prefill(tokens[100:]))
+    # the tiny model's prefill is short, so a cancel thread can miss it: a
+    # call that completed uncancelled is rolled back and tried again
+    for attempt in range(5):
+        m.reset_kv_cache()
+        m.prefill(tokens[:100])
+        try:
+            cancel_while_running(m, lambda: m.prefill(tokens[100:]))
+        except jev.CancelledError:
+            break
+    else:
+        pytest.fail("no cancel reached the prefill in flight in 5 attempts")
     assert m.cached_token_count == 100
     got = m.forward(tokens[100:500])  # continues the 100 cached tokens
     assert np.array_equal(got, want)
