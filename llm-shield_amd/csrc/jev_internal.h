@@ -255,6 +255,9 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 // Decode attention: one query token per entry, split over kDecodeKeys-key
 // chunks; leaves per-chunk partials for the consumer (GemvArgs::attn).
 constexpr int kDecodeKeys = 64;
+// Passes of single-token rows take the decode attention while their chunk
+// partials (rows x chunks of them) stay within this many.
+constexpr int kSingleRowsChunks = 4096;
 struct DecodeAttnArgs {
     int T = 0, n_heads = 0, group = 4, hd = 128, max_chunks = 0;
     const float *q = nullptr;
@@ -265,6 +268,7 @@ struct DecodeAttnArgs {
     const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     float scale = 0.f;
     float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
+    // (T >= 2 needs the per-token arrays and q already rotated: rope_fused 0.)
     // One token (T = 1) with rope_fused: RoPE and the KV store happen here --
     // q from the projection partials of `rope` (q_in / k_in / v_in, nin,
     // in_stride, the frequency and scaling fields), the new key and value
@@ -275,6 +279,20 @@ struct DecodeAttnArgs {
     hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
+
+// Several one-token queries (a pass whose attention tiles are all single
+// tokens: the reasoning decider's rows) through the decode attention: each
+// token's chunk partials merged in ascending chunk order -- the arithmetic of
+// the one-token O GEMV's merge -- and written as the fp16 pair in the
+// operand-tile layout the O projection's GEMM reads.
+struct AttnCombineArgs {
+    int T = 0, n_heads = 0, max_chunks = 0;
+    const float *part = nullptr; // [T][heads][max_chunks][130]
+    const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
+    uint16_t *ot = nullptr; // [T16][heads * 128] pair tiles
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+};
+hipError_t launch_attn_combine(const AttnCombineArgs &a, hipStream_t s);
 
 // Verdict-row head: for each output b, logits[b][i] = dot(norm(h[outputs[b]]), W[rows[i]]).
 struct HeadRowsArgs {

@@ -661,8 +661,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.T != 1) return hipErrorInvalidValue; // one token: its consumer reads entry 0
+    // several tokens: each its own layout entry, q rotated beforehand
+    if (a.T > 1 && (a.rope_fused || !a.slot || !a.shared_lo || !a.shared_hi || !a.segment)) return hipErrorInvalidValue;
     if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
+    if (!a.rope.q_in || !a.rope.k_in || !a.rope.v_in || !a.rope.freqs || a.rope.nin < 1) return hipErrorInvalidValue;
     if (a.rope_fused && (a.T != 1 || a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
                          !a.rope.k_in || !a.rope.v_in || !a.rope.kc || !a.rope.vc || !a.rope.kp || !a.rope.vp ||
                          !a.rope.freqs || a.rope.kc != a.kc || a.rope.vc != a.vc))
@@ -671,6 +673,62 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
                    a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+// One workgroup of 64 lanes per (token, head): lane l merges dims 2 l and
+// 2 l + 1 over the token's chunks in ascending order with a running max
+// (each step rescales what came before by exp(old max - new max)), the same
+// operations as the one-token O GEMV's staging, then writes the normalised
+// context as the fp16 pair (hi rounded to nearest, lo the remainder).
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnCombineArgs a)
+{
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int slot = a.slot[t], slo = a.shared_lo[t], shi = a.shared_hi[t], seg = a.segment[t];
+    const int limit = (shi - slo) + (slot - seg + 1);
+    const int nch = min((limit + kDecodeKeys - 1) / kDecodeKeys, a.max_chunks);
+    const float *pp = a.part + ((size_t)t * a.n_heads + h) * a.max_chunks * 130;
+    float M = -INFINITY, L = 0.f, v0 = 0.f, v1 = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 8) {
+        float mv[8], lv[8];
+        float2 ov[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float *pc = pp + min(c0 + j, nch - 1) * 130; // clamped reloads are unused
+            mv[j] = pc[0];
+            lv[j] = pc[1];
+            ov[j] = *(const float2 *)(pc + 2 + 2 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (c0 + j < nch) {
+                const float Mn = fmaxf(M, mv[j]);
+                const float fo = __expf(M - Mn), fc = __expf(mv[j] - Mn);
+                L = fmaf(lv[j], fc, L * fo);
+                v0 = fmaf(ov[j].x, fc, v0 * fo);
+                v1 = fmaf(ov[j].y, fc, v1 * fo);
+                M = Mn;
+            }
+        }
+    }
+    const float inv = 1.0f / L;
+    v0 = v0 * inv;
+    v1 = v1 * inv;
+    uint16_t h0, l0, h1, l1;
+    split_f16(v0, h0, l0);
+    split_f16(v1, h1, l1);
+    const int k = h * 128 + 2 * lane, nblk = a.n_heads * 4;
+    // k and k + 1 are neighbours in the layout (k even)
+    *(uint32_t *)(a.ot + xt_index(t, k, nblk, 0)) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    *(uint32_t *)(a.ot + xt_index(t, k, nblk, 1)) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+}
+
+hipError_t launch_attn_combine(const AttnCombineArgs &a, hipStream_t s)
+{
+    if (a.T <= 0) return hipSuccess;
+    if (a.n_heads < 1 || a.max_chunks < 1 || !a.part || !a.ot || !a.slot || !a.shared_lo || !a.shared_hi || !a.segment)
+        return hipErrorInvalidValue;
+    launch_stamped(a.ev_start, a.ev_stop, attn_combine_kernel, dim3(a.T, a.n_heads), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -411,7 +411,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     return JEV_OK;
 }
 
-int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
+int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks, bool single_rows = false)
 {
     const jev_config &f = c->cfg;
     size_t qkv = (size_t)c->qdim() + 2 * c->kvdim();
@@ -427,6 +427,7 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks)
         HIP_TRY(c->f32.ensure((size_t)2 * f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
     } else {
+        if (single_rows) HIP_TRY(c->part.ensure((size_t)T * f.n_heads * std::max(1, max_chunks) * 130));
         size_t T16 = ((size_t)T + 15) & ~(size_t)15;
         HIP_TRY(c->xt.ensure(T16 * std::max(f.hidden, c->qdim()) * 2));
         HIP_TRY(c->ft.ensure(T16 * f.ffn * 2));
@@ -453,6 +454,9 @@ struct Plan {
     const int32_t *d_tokens = nullptr, *d_slot = nullptr, *d_pos = nullptr, *d_slo = nullptr, *d_shi = nullptr,
                   *d_seg = nullptr, *d_out = nullptr, *d_rows = nullptr;
     int n_tiles = 0;
+    // every attention tile a single token (rows of one token each): the
+    // decode attention serves them, its chunks combined per token
+    bool single_rows = false;
     double visible_pairs = 0; // sum over tokens of visible keys
     double kv_rows = 0;       // distinct cache rows a layer's attention reads
 };
@@ -548,6 +552,7 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
     p.n_tiles = (int)tiles.size();
     p.kv_rows = std::min<double>(p.end, max_limit + (double)T);
     p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys;
+    p.single_rows = L && T >= 2 && p.n_tiles == T && (long)T * std::max(1, p.max_chunks) <= kSingleRowsChunks;
 
     HIP_TRY(c->ints.ensure(H.size() + 1));
     HIP_TRY(c->tiles.ensure(tiles.size() + 1));
@@ -838,6 +843,49 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             HIP_TRY(launch_attn_decode(da, s));
             CAP_TRY(cap_chunks(c, cap, layer_tap(l, "attn_weighted"), c->part.p, p.max_chunks,
                                (p.start + 1 + kDecodeKeys - 1) / kDecodeKeys));
+        } else if (p.single_rows) {
+            // rows of one token: the decode attention per token (q rotated
+            // and the keys stored by rope_store_kernel above), then its chunks
+            // combined into the O projection's pair input
+            DecodeAttnArgs da;
+            da.T = T;
+            da.n_heads = f.n_heads;
+            da.group = group;
+            da.hd = f.head_dim;
+            da.max_chunks = p.max_chunks;
+            da.q = c->q.p;
+            da.kc = kc;
+            da.vc = vc;
+            da.cap = c->cap;
+            da.slot = p.d_slot;
+            da.shared_lo = p.d_slo;
+            da.shared_hi = p.d_shi;
+            da.segment = p.d_seg;
+            da.start = p.start;
+            da.scale = scale;
+            da.part = c->part.p;
+            da.rope_fused = 0;
+            da.rope = ra;
+            {
+                ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
+                             8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs, true);
+                da.ev_start = ps.a;
+                da.ev_stop = ps.z;
+                HIP_TRY(launch_attn_decode(da, s));
+            }
+            AttnCombineArgs ca;
+            ca.T = T;
+            ca.n_heads = f.n_heads;
+            ca.max_chunks = p.max_chunks;
+            ca.part = c->part.p;
+            ca.slot = p.d_slot;
+            ca.shared_lo = p.d_slo;
+            ca.shared_hi = p.d_shi;
+            ca.segment = p.d_seg;
+            ca.ot = c->xt.p;
+            HIP_TRY(launch_attn_combine(ca, s));
+            CAP_TRY(cap_pair(c, cap, layer_tap(l, "attn_weighted"), c->xt.p, T, qdim));
+            if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xt.p, T, qdim, c->xsum.p, s));
         } else {
             AttnArgs aa;
             aa.n_tiles = p.n_tiles;
@@ -1055,7 +1103,7 @@ int prepare(jev_ctx *c, const int32_t *tokens, bool on_device, int T, const jev_
     if (rc) return rc;
     rc = build_plan(c, tokens, on_device, T, layout, mode, rows, n_rows, p);
     if (rc) return rc;
-    return ensure_workspace(c, T, p.n_out, mode, p.max_chunks);
+    return ensure_workspace(c, T, p.n_out, mode, p.max_chunks, p.single_rows);
 }
 
 } // namespace
@@ -1677,7 +1725,7 @@ int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int
     int max_limit = 0;
     for (int r = 0; r < n_rows; r++) max_limit = std::max(max_limit, shared + row_length[r] + n_steps);
     p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys; // grid for the longest step
-    rc = ensure_workspace(c, n_rows, p.n_out, JEV_OUT_FULL, p.max_chunks);
+    rc = ensure_workspace(c, n_rows, p.n_out, JEV_OUT_FULL, p.max_chunks, p.single_rows);
     if (rc) return rc;
     HIP_TRY(c->logits.ensure(std::max(c->logits.n, (size_t)n_rows * c->cfg.vocab)));
     HIP_TRY(c->dec_state.ensure((size_t)n_rows * (n_steps + 1)));
