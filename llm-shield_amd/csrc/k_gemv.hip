@@ -39,6 +39,16 @@ struct RawTile {
     uint32_t qh;   // Q5_1: two bytes (block 0 low byte)
 };
 
+// Bit i of a 4-bit value x << 4 to bit 8 i + 4 (masked by the caller):
+// (x << 4) * 0x204081 (both fit 24 bits) on the full-rate 24-bit multiplier
+// (the compiler picks the quarter-rate 32-bit one for the plain product).
+__device__ __forceinline__ uint32_t spread4(uint32_t x)
+{
+    uint32_t r;
+    asm("v_mul_u32_u24 %0, %1, %2" : "=v"(r) : "v"(x), "v"(0x00204081u));
+    return r;
+}
+
 // B fragment of block bb of the tile: 8 fp16 integers for k = 8g .. 8g + 7.
 template <int TYPE>
 __device__ __forceinline__ half8_t decode_frag(const RawTile &t, int bb)
@@ -54,8 +64,8 @@ __device__ __forceinline__ half8_t decode_frag(const RawTile &t, int bb)
         _Float16 bias = (_Float16)1032.0f;
         if (TYPE == kQ5_1) {
             const uint32_t hb = (t.qh >> (8 * bb)) & 0xffu;
-            n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
-            n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
+            n0 |= spread4((hb & 15u) << 4) & 0x10101010u;
+            n1 |= spread4(hb & 0xf0u) & 0x10101010u;
             bias = (_Float16)1024.0f;
         }
         bytes_to_f16(n0, bias, o0, o1);
@@ -87,24 +97,28 @@ struct TileLoader {
         tile0 = min(rg, RG - 1) * KP; // groups past the weight feed unstored outputs
     }
 
-    __device__ RawTile load(int kp) const
+    // ok false: a tile past the wave's range -- its lane offsets point past
+    // every buffer, so the loads return zeros (quants, scales and mins) and
+    // the tile adds 0 * p without a mask
+    __device__ RawTile load(int kp, bool ok) const
     {
         RawTile t;
         const int tile = tile0 + kp;
+        const uint32_t past = ok ? 0u : 0x80000000u;
         if (TYPE == kQ8_0) {
-            t.q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, vq, tile * 1024, 0));
+            t.q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, vq + past, tile * 1024, 0));
         } else {
-            uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, vq, tile * 512, 0));
+            uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, vq + past, tile * 512, 0));
             t.q = make_uint4(v.x, v.y, 0u, 0u);
         }
         if (TYPE == kQ5_1) {
             // the row's scales and mins in one load
-            const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd, 2 * vd, tile * 128, 0));
+            const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd, 2 * vd + past, tile * 128, 0));
             t.d = dm.x;
             t.m = dm.y;
-            t.qh = __builtin_amdgcn_raw_buffer_load_b16(rh, vh, tile * 128, 0);
+            t.qh = __builtin_amdgcn_raw_buffer_load_b16(rh, vh + past, tile * 128, 0);
         } else {
-            t.d = __builtin_amdgcn_raw_buffer_load_b32(rd, vd, tile * 64, 0);
+            t.d = __builtin_amdgcn_raw_buffer_load_b32(rd, vd + past, tile * 64, 0);
         }
         return t;
     }
@@ -156,9 +170,10 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
     auto load_stage = [&](int st, RawTile (&r)[NW][DEPTH]) {
 #pragma unroll
         for (int j = 0; j < DEPTH; j++) {
-            const int kp = kp0 + max(0, min(st * DEPTH + j, ntiles - 1)); // clamped: reloads feed no output
+            const int tl = st * DEPTH + j;
+            const int kp = kp0 + max(0, min(tl, ntiles - 1)); // in range; past the wave's tiles the loads read zeros
 #pragma unroll
-            for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp);
+            for (int w = 0; w < NW; w++) r[w][j] = ld[w].load(kp, tl < ntiles);
         }
     };
     // x of the first kPre groups of 256 is loaded before the first stage's
@@ -316,7 +331,6 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
 #pragma unroll
         for (int j = 0; j < DEPTH; j++) {
             const int tl = st * DEPTH + j; // tile within the wave's range
-            const bool valid = tl < ntiles;
             const int lt = t0 + min(tl, ntiles - 1); // tile within the workgroup's range
 #pragma unroll
             for (int bb = 0; bb < 2; bb++) {
@@ -325,11 +339,11 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
                 for (int w = 0; w < NW; w++) {
                     const half8_t bf = decode_frag<TYPE>(r[w][j], bb);
                     floatx4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    const float dv = valid ? half_of(r[w][j].d, bb) : 0.f;
+                    const float dv = half_of(r[w][j].d, bb); // 0 past the range
                     const float v = p[0] + p[1];
                     acc[w] = fmaf(dv, v, acc[w]);
                     if (TYPE == kQ5_1) {
-                        const float mv = valid ? half_of(r[w][j].m, bb) : 0.f;
+                        const float mv = half_of(r[w][j].m, bb);
                         acc[w] = fmaf(mv, xsum[2 * lt + bb], acc[w]);
                     }
                 }
