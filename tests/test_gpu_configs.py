@@ -142,3 +142,36 @@ def test_q5_1_decode_after_a_512_token_prompt(gpu):
             note(f"{steps} decode steps over {len(prompt)}..{len(prompt) + steps} keys match the oracle")
     finally:
         ref.close()
+
+
+def test_q5_1_rows_of_one_token_after_prompts_alone(gpu):
+    # The reasoning decider's rows (ReasoningDecider.cs:134-174) at full shape:
+    # prompts of 64, 150, 256 and 300 tokens, each prefilled alone into its
+    # row, then one-token steps of all four rows (2 to 5 chunks of 64 keys per
+    # token, merged per token) against the oracle's full-vocabulary logits.
+    synth = jev.SynthModel(jev.ModelConfig(initial_kv_capacity=1024), jev.TYPE_Q5_1)
+    lengths = [64, 150, 256, 300]
+    prompts = [list(jev.random_tokens(n, VOCAB, 80 + i)) for i, n in enumerate(lengths)]
+    steps = 2
+    bases = jev.row_bases(lengths, steps + 1)
+    ref = host_oracle(synth)
+    try:
+        with synth.open(0) as m:
+            nxt = []
+            for r, p in enumerate(prompts):
+                z = m.forward_rows(0, [bases[r]], [0], [p])[0]
+                e = ref.forward_layout(p, jev.TokenLayout.rows(0, [bases[r]], [0], [len(p)]), oracle.OUT_FULL)
+                assert worst_close(e, z) <= 1e-3, r
+                nxt.append(jev.index_of_max(z))
+            note("four prompts prefilled alone into their rows match the oracle")
+            lens = list(lengths)
+            for i in range(steps):
+                g = np.array(m.forward_rows(0, bases, lens, [[t] for t in nxt]))
+                lay = jev.TokenLayout.rows(0, bases, lens, [1] * len(lens))
+                e = ref.forward_layout(nxt, lay, oracle.OUT_FULL).reshape(len(lens), -1)
+                assert worst_close(e, g) <= 1e-3, i
+                lens = [n + 1 for n in lens]
+                nxt = [jev.index_of_max(z) for z in g]
+            note(f"{steps} one-token steps of {len(lens)} rows match the oracle")
+    finally:
+        ref.close()

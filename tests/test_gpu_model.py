@@ -193,6 +193,25 @@ def test_rows_layout_batched_decode(model, ref):
     assert worst_close(e, np.array(g)) <= 1e-3
 
 
+def test_rows_of_one_token_over_several_key_chunks(model, ref):
+    # Rows of different lengths after a 150-token prefix, then one token per
+    # row: 156, 211 and 261 visible keys, i.e. 3, 4 and 5 chunks of 64 merged
+    # per token (the per-token decode attention and its chunk combine).
+    shared = jev.random_tokens(150, 2048, 17)
+    fresh(model).prefill(shared)
+    fresh(ref).prefill(shared)
+    bases, lengths = [150, 160, 230], [5, 60, 110]
+    prompts = [list(jev.random_tokens(n, 2048, 18 + n)) for n in lengths]
+    model.forward_rows(150, bases, [0, 0, 0], prompts, ROWS)
+    lay = jev.TokenLayout.rows(150, bases, [0, 0, 0], lengths)
+    ref.forward_layout(np.concatenate(prompts).astype(np.int32), lay, oracle.OUT_SELECTED, ROWS)
+    step = [7, 11, 1500]
+    g = model.forward_rows(150, bases, lengths, [[t] for t in step])
+    lay = jev.TokenLayout.rows(150, bases, lengths, [1, 1, 1])
+    e = ref.forward_layout(step, lay, oracle.OUT_FULL).reshape(3, -1)
+    assert worst_close(e, np.array(g)) <= 1e-3
+
+
 def test_greedy_decode_follows_oracle(model, ref):
     tokens = jev.random_tokens(30, 2048, 16)
     fresh(model).prefill(tokens)
