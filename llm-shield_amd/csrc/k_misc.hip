@@ -187,24 +187,46 @@ hipError_t launch_rmsnorm(const NormArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
-__global__ void block_sums_kernel(const uint16_t *xt, int D, float *xsum)
+// Q5_1 block sums of an operand tile buffer: per row t and 32-block b, the
+// sum of (hi + lo) over the block's 32 values in ascending k -- the term the
+// Q5_1 min multiplies.  One thread per (row, block); the block's hi and lo
+// parts are four 16-byte slots each (slot q holds k = 8 q .. 8 q + 7), and the
+// 16 rows of a row group are neighbouring threads, so each slot load is a
+// contiguous 256 bytes across them.
+__global__ __launch_bounds__(256) void block_sums_kernel(const uint16_t *xt, int T, int nb, float *xsum)
 {
-    int t = blockIdx.x;
-    int nb = D >> 5;
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-        float s = 0.f;
-        for (int j = 0; j < 32; j++) {
-            int k = b * 32 + j;
-            s += h2f(xt[xt_index(t, k, nb, 0)]) + h2f(xt[xt_index(t, k, nb, 1)]);
-        }
-        xsum[(size_t)t * nb + b] = s;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int r = i & 15, gb = i >> 4; // gb = row group * nb + block
+    const int rg = gb / nb, b = gb - rg * nb;
+    const int t = rg * 16 + r;
+    if (t >= T) return;
+    const uint4 *base = (const uint4 *)xt + (size_t)gb * 2 * 64 + r;
+    uint4 h[4], l[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        h[q] = base[16 * q];
+        l[q] = base[64 + 16 * q];
     }
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint32_t hw[4] = {h[q].x, h[q].y, h[q].z, h[q].w}, lw[4] = {l[q].x, l[q].y, l[q].z, l[q].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint16_t hv = (uint16_t)(hw[e >> 1] >> (16 * (e & 1))), lv = (uint16_t)(lw[e >> 1] >> (16 * (e & 1)));
+            sum += h2f(hv) + h2f(lv);
+        }
+    }
+    xsum[(size_t)t * nb + b] = sum;
 }
 
 hipError_t launch_block_sums(const uint16_t *xt, int T, int D, float *xsum, hipStream_t s)
 {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(block_sums_kernel, dim3(T), dim3(128), 0, s, xt, D, xsum);
+    if (D % 32 != 0) return hipErrorInvalidValue;
+    const int nb = D >> 5;
+    const long threads = (long)((T + 15) / 16) * nb * 16;
+    hipLaunchKernelGGL(block_sums_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, xt, T, nb, xsum);
     return hipGetLastError();
 }
 
