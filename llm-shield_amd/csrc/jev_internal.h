@@ -290,6 +290,7 @@ struct AttnCombineArgs {
     const float *part = nullptr; // [T][heads][max_chunks][130]
     const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
     uint16_t *ot = nullptr; // [T16][heads * 128] pair tiles
+    float *xsum = nullptr;  // [T][heads * 4] block sums of ot (Q5_1 projections), or null
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
 };
 hipError_t launch_attn_combine(const AttnCombineArgs &a, hipStream_t s);

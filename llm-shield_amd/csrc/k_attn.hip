@@ -721,6 +721,20 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnCombineArgs a)
     // k and k + 1 are neighbours in the layout (k even)
     *(uint32_t *)(a.ot + xt_index(t, k, nblk, 0)) = (uint32_t)h0 | ((uint32_t)h1 << 16);
     *(uint32_t *)(a.ot + xt_index(t, k, nblk, 1)) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    if (a.xsum) {
+        // the Q5_1 block sums of these pairs, in the order the block-sum
+        // kernel adds an operand tile's values (ascending k, hi + lo per
+        // element): block q of the head is lanes 16 q .. 16 q + 15
+        const float e0 = h2f(h0) + h2f(l0), e1 = h2f(h1) + h2f(l1);
+        const int q0 = lane & 48;
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            sum += __shfl(e0, q0 + i, 64);
+            sum += __shfl(e1, q0 + i, 64);
+        }
+        if ((lane & 15) == 0) a.xsum[(size_t)t * nblk + h * 4 + (lane >> 4)] = sum;
+    }
 }
 
 hipError_t launch_attn_combine(const AttnCombineArgs &a, hipStream_t s)

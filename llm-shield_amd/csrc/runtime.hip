@@ -883,9 +883,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             ca.shared_hi = p.d_shi;
             ca.segment = p.d_seg;
             ca.ot = c->xt.p;
+            ca.xsum = L.o.type == kQ5_1 ? c->xsum.p : nullptr;
             HIP_TRY(launch_attn_combine(ca, s));
             CAP_TRY(cap_pair(c, cap, layer_tap(l, "attn_weighted"), c->xt.p, T, qdim));
-            if (L.o.type == kQ5_1) HIP_TRY(launch_block_sums(c->xt.p, T, qdim, c->xsum.p, s));
         } else {
             AttnArgs aa;
             aa.n_tiles = p.n_tiles;
