@@ -661,11 +661,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    // several tokens: each its own layout entry, q rotated beforehand
-    if (a.T > 1 && (a.rope_fused || !a.slot || !a.shared_lo || !a.shared_hi || !a.segment)) return hipErrorInvalidValue;
+    // several tokens: each its own layout entry (and position, when RoPE is
+    // fused: the caller guarantees no token sees another's new key)
+    if (a.T > 1 && (!a.slot || !a.shared_lo || !a.shared_hi || !a.segment || (a.rope_fused && !a.rope.pos)))
+        return hipErrorInvalidValue;
     if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
     if (!a.rope.q_in || !a.rope.k_in || !a.rope.v_in || !a.rope.freqs || a.rope.nin < 1) return hipErrorInvalidValue;
-    if (a.rope_fused && (a.T != 1 || a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
+    if (a.rope_fused && (a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
                          !a.rope.k_in || !a.rope.v_in || !a.rope.kc || !a.rope.vc || !a.rope.kp || !a.rope.vp ||
                          !a.rope.freqs || a.rope.kc != a.kc || a.rope.vc != a.vc))
         return hipErrorInvalidValue;

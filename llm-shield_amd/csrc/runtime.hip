@@ -457,6 +457,10 @@ struct Plan {
     // every attention tile a single token (rows of one token each): the
     // decode attention serves them, its chunks combined per token
     bool single_rows = false;
+    // ... and no token sees another's key from this pass (rows: each sees the
+    // cached prefix and its own row): each token's RoPE and KV store can run
+    // inside its own decode attention, as for one token
+    bool rows_independent = false;
     double visible_pairs = 0; // sum over tokens of visible keys
     double kv_rows = 0;       // distinct cache rows a layer's attention reads
 };
@@ -553,6 +557,17 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
     p.kv_rows = std::min<double>(p.end, max_limit + (double)T);
     p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys;
     p.single_rows = L && T >= 2 && p.n_tiles == T && (long)T * std::max(1, p.max_chunks) <= kSingleRowsChunks;
+    if (p.single_rows) {
+        std::vector<int32_t> fresh(L->slot, L->slot + T);
+        std::sort(fresh.begin(), fresh.end());
+        auto any_in = [&](int a, int b) { // a slot of this pass in [a, b)
+            return a < b && std::lower_bound(fresh.begin(), fresh.end(), b) - std::lower_bound(fresh.begin(), fresh.end(), a) > 0;
+        };
+        bool ok = true;
+        for (int t = 0; t < T && ok; t++)
+            ok = !any_in(L->shared_lo[t], L->shared_hi[t]) && !any_in(L->segment[t], L->slot[t]);
+        p.rows_independent = ok;
+    }
 
     HIP_TRY(c->ints.ensure(H.size() + 1));
     HIP_TRY(c->tiles.ensure(tiles.size() + 1));
@@ -799,8 +814,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.mscale = c->mscale;
         ra.orig_ctx = f.rope_original_context;
         ra.temp_scale = f.attention_temperature_scale;
-        // one token: RoPE and the KV store run inside the decode attention kernel
-        if (T != 1 || cap) HIP_TRY(launch_rope_store(ra, s));
+        // one token, or rows of one token that see none of each other's keys:
+        // RoPE and the KV store run inside the decode attention kernel
+        const bool rows_fused = p.single_rows && p.rows_independent && !cap;
+        if ((T != 1 && !rows_fused) || cap) HIP_TRY(launch_rope_store(ra, s));
         CAP_TRY(cap_add(c, cap, layer_tap(l, "q_rope"), c->q.p, T, qdim));
         CAP_TRY(cap_kv(c, cap, layer_tap(l, "k_rope"), kc, p.start, T));
         CAP_TRY(cap_kv(c, cap, layer_tap(l, "v"), vc, p.start, T));
@@ -844,8 +861,9 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             CAP_TRY(cap_chunks(c, cap, layer_tap(l, "attn_weighted"), c->part.p, p.max_chunks,
                                (p.start + 1 + kDecodeKeys - 1) / kDecodeKeys));
         } else if (p.single_rows) {
-            // rows of one token: the decode attention per token (q rotated
-            // and the keys stored by rope_store_kernel above), then its chunks
+            // rows of one token: the decode attention per token (RoPE and the
+            // KV store inside it, or by rope_store_kernel above when tokens
+            // see each other's keys or taps are captured), then its chunks
             // combined into the O projection's pair input
             DecodeAttnArgs da;
             da.T = T;
@@ -864,7 +882,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.start = p.start;
             da.scale = scale;
             da.part = c->part.p;
-            da.rope_fused = 0;
+            da.rope_fused = rows_fused ? 1 : 0;
             da.rope = ra;
             {
                 ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,

@@ -212,6 +212,20 @@ def test_rows_of_one_token_over_several_key_chunks(model, ref):
     assert worst_close(e, np.array(g)) <= 1e-3
 
 
+def test_single_token_tiles_that_see_each_other(model, ref):
+    # A one-token trunk and one-token branches: every attention tile is one
+    # token, but the branches see the trunk token written by the same pass,
+    # so its key must be stored before any token's attention runs.
+    prefix = jev.random_tokens(40, 2048, 19)
+    fresh(model).prefill(prefix)
+    fresh(ref).prefill(prefix)
+    lay = jev.TokenLayout.tree(40, 1, [1, 2, 3], 4)
+    toks = [5, 900, 77, 1234]
+    g = model.forward_layout(toks, lay, jev.OUT_FULL).reshape(3, -1)
+    e = ref.forward_layout(toks, lay, oracle.OUT_FULL).reshape(3, -1)
+    assert worst_close(e, g) <= 1e-3
+
+
 def test_greedy_decode_follows_oracle(model, ref):
     tokens = jev.random_tokens(30, 2048, 16)
     fresh(model).prefill(tokens)

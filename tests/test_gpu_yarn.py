@@ -110,3 +110,23 @@ def test_greedy_decode_graph_follows_oracle(model, ref):
         e = ref.forward([nxt])
         assert e[tok] >= e.max() - 2e-3
         nxt = int(tok)
+
+
+def test_rows_of_one_token_across_the_window(model, ref):
+    # Rows of one token each (RoPE, temperature and the KV store inside the
+    # per-token decode attention) at positions on both sides of n_orig = 64
+    # and past 128: each row's logits against the oracle's.
+    shared = jev.random_tokens(50, 2048, 23)
+    model.reset_kv_cache()
+    ref.reset_kv_cache()
+    model.prefill(shared)
+    ref.prefill(shared)
+    bases, lengths = [50, 70, 150], [3, 20, 90]
+    prompts = [list(jev.random_tokens(n, 2048, 24 + n)) for n in lengths]
+    model.forward_rows(50, bases, [0, 0, 0], prompts, ROWS)
+    ref.forward_layout(np.concatenate(prompts).astype(np.int32), jev.TokenLayout.rows(50, bases, [0, 0, 0], lengths),
+                       oracle.OUT_SELECTED, ROWS)
+    step = [9, 400, 1999]
+    g = np.array(model.forward_rows(50, bases, lengths, [[t] for t in step]))
+    e = ref.forward_layout(step, jev.TokenLayout.rows(50, bases, lengths, [1, 1, 1]), oracle.OUT_FULL).reshape(3, -1)
+    assert worst_close(e, g) <= 1e-3
