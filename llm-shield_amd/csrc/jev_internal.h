@@ -91,6 +91,7 @@ struct GemmArgs {
     float *y = nullptr;
     int ksplit = 1;                      // store mode: K in ksplit ranges, partial z at y + z*M*ldy
     uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
+    float *osum = nullptr;               // SwiGLU at M <= 16: per-32 block sums of ot [M][seg[0].rows / 32], or null
     int mode = kGemmStore;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr; // optional dispatch-stamped timing
 };

@@ -963,9 +963,9 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
     }
 
     // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16].
-    if (g >= ngroups) return;
     const int row_base = 4 * (lane >> 4);
     if (MODE == kGemmStore) {
+        if (g >= ngroups) return;
         const QWeight &ws = a.seg[seg_store];
         if (g * 16 - start_store + (lane & 15) >= ws.rows) return;
         float *y = a.y + (size_t)z * M * a.ldy + g * 16 + (lane & 15);
@@ -975,11 +975,11 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
     } else {
         const int ld = a.seg[0].rows;
         const int col = g * 16 + (lane & 15);
-        if (col >= ld) return;
+        const bool live = g < ngroups && col < ld;
+        __shared__ float es[16 * 64]; // [row][column of the workgroup's 64]: hi + lo of each output
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int row = row_base + r;
-            if (row >= M) continue;
             // Kernels.SwiGlu (Kernels.cs:82-89): (g*u) * sigmoid(g).
             const float gv = acc[0][r], u = acc[1][r];
             const float gu = gv * u;
@@ -988,8 +988,24 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
             const float v = sg * gu;
             uint16_t hi, lo;
             split_f16(v, hi, lo);
-            a.ot[xt_index(row, col, ld >> 5, 0)] = hi;
-            a.ot[xt_index(row, col, ld >> 5, 1)] = lo;
+            if (live && row < M) {
+                a.ot[xt_index(row, col, ld >> 5, 0)] = hi;
+                a.ot[xt_index(row, col, ld >> 5, 1)] = lo;
+            }
+            if (a.osum) es[row * 64 + wave * 16 + (lane & 15)] = h2f(hi) + h2f(lo);
+        }
+        if (a.osum) {
+            // the Q5_1 block sums of these outputs for the down projection: the
+            // workgroup's four row groups are 64 consecutive columns, two whole
+            // blocks (ld is a multiple of 32), each summed in ascending column
+            // order as the block-sum kernel sums an operand tile
+            __syncthreads();
+            const int row = tid & 15, blk = tid >> 4, c0 = q * 64 + 32 * blk;
+            if (tid < 32 && row < M && c0 < ld) {
+                float sum = 0.f;
+                for (int j = 0; j < 32; j++) sum += es[row * 64 + 32 * blk + j];
+                a.osum[(size_t)row * (ld >> 5) + (c0 >> 5)] = sum;
+            }
         }
     }
 }
@@ -1106,6 +1122,7 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s)
     }
     if (a.mode == kGemmSwiGlu && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows || a.seg[0].rows % 32 != 0))
         return hipErrorInvalidValue;
+    if (a.osum && (a.mode != kGemmSwiGlu || a.M > 16)) return hipErrorInvalidValue; // written by the skinny kernel only
     switch (a.seg[0].type) {
     case kQ8_0: return launch_typed<kQ8_0>(a, s);
     case kQ4_0: return launch_typed<kQ4_0>(a, s);

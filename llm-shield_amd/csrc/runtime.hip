@@ -421,7 +421,10 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks, boo
     HIP_TRY(c->yo.ensure((size_t)T * f.hidden * c->split_o(T)));
     HIP_TRY(c->ydown.ensure((size_t)T * f.hidden * c->split_down(T)));
     HIP_TRY(c->q.ensure((size_t)T * c->qdim()));
-    HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + 1));
+    // [0, T * wide / 32): the block sums a GEMM reads; past it, the SwiGLU
+    // output's, written by the small-batch SwiGLU GEMM while it still reads
+    // its own input's
+    HIP_TRY(c->xsum.ensure((size_t)std::max(T, n_out) * wide / 32 + (T <= 16 ? (size_t)T * f.ffn / 32 : 0) + 1));
     if (T == 1) {
         HIP_TRY(c->x32.ensure((size_t)std::max<size_t>(f.hidden, 1)));
         HIP_TRY(c->f32.ensure((size_t)2 * f.ffn));
@@ -946,6 +949,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         CAP_TRY(cap_add(c, cap, layer_tap(l, "ffn_norm"), nf.out32, T, D));
 
         const bool gu_rows = T == 1 && L.gate.type == L.up.type && f.ffn % 16 == 0;
+        const float *down_sums = c->xsum.p;
         if (gu_rows) {
             // one token: gate and up rows as one GEMV of 2 x ffn rows (twice the
             // workgroups of the fused SwiGLU GEMV, so the GPU fills evenly); the
@@ -978,6 +982,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             g.seg[1] = L.up;
             g.mode = kGemmSwiGlu;
             g.ot = c->ft.p;
+            // up to 16 tokens the SwiGLU GEMM also forms the down projection's
+            // Q5_1 block sums
+            if (L.down.type == kQ5_1 && T <= 16)
+                g.osum = c->xsum.p + (size_t)T * std::max<size_t>({(size_t)f.hidden, (size_t)c->qdim(), (size_t)f.ffn}) / 32;
             {
                 ProfScope ps(c, JEV_PROF_GEMM, 4.0 * T * f.ffn * D,
                              weight_bytes(L.gate) + weight_bytes(L.up) + T * (4.0 * D + 4.0 * f.ffn), true);
@@ -985,11 +993,12 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
                 g.ev_stop = ps.z;
                 HIP_TRY(launch_gemm(g, s));
             }
-            if (L.down.type == kQ5_1) HIP_TRY(launch_block_sums(c->ft.p, T, f.ffn, c->xsum.p, s));
+            if (L.down.type == kQ5_1 && !g.osum) HIP_TRY(launch_block_sums(c->ft.p, T, f.ffn, c->xsum.p, s));
+            down_sums = g.osum ? g.osum : c->xsum.p;
         }
         {
             const QWeight *wd[1] = {&L.down};
-            int rc = linear(c, T, wd, 1, c->ft.p, c->xsum.p, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
+            int rc = linear(c, T, wd, 1, c->ft.p, down_sums, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
             if (rc) return rc;
         }
         CAP_TRY(cap_partials(c, cap, layer_tap(l, "ffn_out"), c->ydown.p, s_down, T, D));

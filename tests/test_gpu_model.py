@@ -109,6 +109,25 @@ def test_tree_equals_branches_alone_bitwise(model):
         assert np.array_equal(alone[b], cached[b]), b
 
 
+@pytest.mark.parametrize("t", [jev.TYPE_Q5_1, jev.TYPE_Q4_0])
+def test_tree_equals_branches_alone_bitwise_other_types(gpu, t):
+    # Branches of 2..16 tokens alone take the small-batch GEMM (which, for
+    # Q5_1, also forms the down projection's block sums); in the tree they
+    # take the wide one and the block-sum kernel.  The bits must agree.
+    synth = jev.SynthModel(tiny_config(), t)
+    prefix = jev.random_tokens(90, 2048, 28)
+    branches = [jev.random_tokens(n, 2048, 60 + n) for n in (30, 2, 9, 16)]
+    with synth.open(0) as m:
+        m.prefill(prefix)
+        alone = []
+        for b in branches:
+            m.kv_truncate(len(prefix))
+            alone.append(m.forward_selected(b, ROWS))
+        tree = fresh(m).forward_tree(prefix, branches, ROWS)
+    for b in range(len(branches)):
+        assert np.array_equal(alone[b], tree[b]), b
+
+
 @pytest.mark.parametrize("trunk", [2100, 4100])
 def test_tree_equals_branches_alone_across_attention_grids(model, trunk):
     # The attention grid has one workgroup per 32-token tile and KV head; grids
