@@ -869,7 +869,11 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
                 const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[n], 2 * vd, tile * 128, 0));
                 br[n].d = dm.x;
                 br[n].m = dm.y;
-                br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
+                // the aligned word holding the lane's two bytes, shifted where
+                // it is decoded: a 16-bit load's zero-extension is an
+                // instruction the compiler hoists into an earlier stage, where
+                // it waits on the whole ring behind it
+                br[n].qh = __builtin_amdgcn_raw_buffer_load_b32(rh[n], vh & ~3u, tile * 128, 0);
             } else {
                 br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
             }
@@ -895,9 +899,13 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
     // Chunk c's block sums, thread t: block t / 16 of the chunk, row t % 16
     // (the address gemm_bd_kernel reads for that row and block).
     auto load_xs = [&](int c) __attribute__((always_inline)) -> float {
-        if (TYPE != kQ5_1 || tid >= CH * 32) return 0.f;
-        const int bl = tid >> 4, st = min(c * CH + (bl >> 1), nstage - 1);
-        const uint32_t off = ((uint32_t)(tid & 15) * nblk + kb_begin + 2 * st + (bl & 1)) * 4;
+        if (TYPE != kQ5_1) return 0.f;
+        // every thread loads (threads past CH * 32 a clamped entry nobody
+        // stores): a branch around the load would cost the compiler its count
+        // of the loads in flight, and a full drain at each chunk's first stage
+        const int e = min(tid, CH * 32 - 1);
+        const int bl = e >> 4, st = min(c * CH + (bl >> 1), nstage - 1);
+        const uint32_t off = ((uint32_t)(e & 15) * nblk + kb_begin + 2 * st + (bl & 1)) * 4;
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
     };
 
@@ -915,7 +923,9 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
             if (TYPE == kQ5_1) xs4 = *(const floatx4 *)&Xs[buf][(sl * 2 + bb) * 16 + 4 * (lane >> 4)];
 #pragma unroll
             for (int n = 0; n < TN; n++) {
-                const half8_t bf = decode_b_frag<TYPE>(br[n], bb);
+                BChunk c = br[n];
+                if (TYPE == kQ5_1) c.qh >>= 8 * (vh & 2); // odd lanes: the word's high half
+                const half8_t bf = decode_b_frag<TYPE>(c, bb);
                 const float dv = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d))) & live);
                 float mv = 0.f;
                 if (TYPE == kQ5_1)
