@@ -354,11 +354,18 @@ __global__ __launch_bounds__(256, 2) void gemv_q_kernel(GemvArgs a, int nrows, i
     // Two register stages; whole pairs in the loop, the odd stage after it.
     if (nst > 0) {
         int st = 0;
+        // sched_barriers at the stage boundaries: the scheduler would hoist
+        // parts of the next stage's decode into this stage's compute, where
+        // they wait on loads issued moments before
         for (; st + 2 <= nst; st += 2) {
             load_stage(st + 1, r1);
+            __builtin_amdgcn_sched_barrier(0);
             compute_stage(st, r0);
+            __builtin_amdgcn_sched_barrier(0);
             load_stage(st + 2, r0);
+            __builtin_amdgcn_sched_barrier(0);
             compute_stage(st + 1, r1);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (st < nst) compute_stage(st, r0);
     }
