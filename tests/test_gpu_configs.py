@@ -175,3 +175,28 @@ def test_q5_1_rows_of_one_token_after_prompts_alone(gpu):
             note(f"{steps} one-token steps of {len(lens)} rows match the oracle")
     finally:
         ref.close()
+
+
+def test_q5_1_rows_graph_is_the_step_by_step_loop(gpu):
+    # The reasoning decider's rows at full shape, as bench.py runs them (12 rows,
+    # each prompt prefilled alone): the replayed rows graph gives the tokens of
+    # one forward_rows call per step, bit for bit.
+    synth = jev.SynthModel(jev.ModelConfig(initial_kv_capacity=2048), jev.TYPE_Q5_1)
+    n_rows, plen, steps = 12, 64, 6
+    prompts = [list(jev.random_tokens(plen, VOCAB, 50 + r)) for r in range(n_rows)]
+    bases = jev.row_bases([plen] * n_rows, steps + 1)
+    with synth.open(0) as m:
+        def start():
+            m.reset_kv_cache()
+            return [jev.index_of_max(m.forward_rows(0, [bases[r]], [0], [prompts[r]])[0]) for r in range(n_rows)]
+        first = start()
+        graph = m.decode_rows_greedy(0, bases, [plen] * n_rows, first, steps)
+        assert start() == first
+        lengths, nxt, loop = [plen] * n_rows, list(first), []
+        for _ in range(steps):
+            z = m.forward_rows(0, bases, lengths, [[t] for t in nxt])
+            lengths = [n + 1 for n in lengths]
+            nxt = [jev.index_of_max(v) for v in z]
+            loop.append(nxt)
+    assert np.array_equal(graph, np.array(loop, np.int32))
+    note(f"{n_rows} rows x {steps} steps: graph == step-by-step loop")
