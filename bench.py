@@ -533,6 +533,29 @@ def main():
     gemv = prof_read(lib, h, L.PROF_GEMV)
     L.check(lib.jev_profile_enable(h, 0))
 
+    # The boundary the managed host binds (ForwardAsync, Benchmark.cs:406-409):
+    # jev_forward with host token ids and host logits, its per-layer
+    # cancellation throttle included, one synchronous call per prefill.
+    h_tok = np.ascontiguousarray(tokens, np.int32)
+    h_logits = np.empty(cfg.vocab, np.float32)
+
+    def host_step():
+        L.check(lib.jev_kv_reset(h))
+        L.check(lib.jev_forward(h, h_tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), T, None, L.OUT_LAST_FULL,
+                                None, 0, h_logits.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), h_logits.size))
+
+    for _ in range(max(1, args.warmup)):
+        host_step()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        host_step()
+    host_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    log(f"prefill through jev_forward (host buffers, throttled): {host_ms:.3f} ms/step "
+        f"({(host_ms / ms_step - 1) * 100:+.1f} % against the device-buffer call)")
+    boundary = {"prefill_jev_forward_ms": round(host_ms, 4), "prefill_jev_forward_tok_s": round(T / host_ms * 1e3, 1),
+                "prefill_extra_pct": round((host_ms / ms_step - 1) * 100, 2),
+                "logits_equal_device_call": bool(np.array_equal(h_logits, gpu_logits))}
+
     gemm_avg_ms = gemm[1] / max(gemm[0], 1)
     gemm_tflops = gemm[2] / (gemm[1] * 1e-3) / 1e12 if gemm[1] > 0 else 0.0
     log(f"GEMM: {gemm[0]} launches, {gemm[1]:.2f} ms, {gemm_tflops:.1f} TFLOP/s algorithmic")
@@ -579,6 +602,7 @@ def main():
             "attention": round(attn[1] / prof_steps, 4),
             "gemv_head": round(gemv[1] / prof_steps, 4),
         },
+        "boundary": boundary,
     }
 
     # ---- tree decision (4096 trunk + 9 x 48 branches, verdict rows only)
@@ -607,6 +631,20 @@ def main():
         L.check(lib.jev_sync(h))
         torch.cuda.synchronize()
         tree_ms = (time.perf_counter() - t0) / args.tree_steps * 1e3
+        # the same decision through jev_forward_tree (ForwardTreeAsync, JevstralDecider.cs:300):
+        # host token ids and verdict rows, the per-layer throttle included
+        trunk_h = toks[:trunk_n]
+        branches_h = [toks[trunk_n + b * bl: trunk_n + (b + 1) * bl] for b in range(nb)]
+
+        def decide_host():
+            L.check(lib.jev_kv_reset(h))
+            return model.forward_tree(trunk_h, branches_h, rows)
+
+        decide_host()
+        t0 = time.perf_counter()
+        for _ in range(args.tree_steps):
+            vh = decide_host()
+        tree_host_ms = (time.perf_counter() - t0) / args.tree_steps * 1e3
         L.check(lib.jev_profile_enable(h, 1))
         for _ in range(args.tree_steps):
             decide()
@@ -625,6 +663,10 @@ def main():
             "attention_tflops": round(ta[2] / (ta[1] * 1e-3) / 1e12, 2) if ta[1] else None,
         }
         result["tree_z"] = [round(float(x), 5) for x in z]
+        result["boundary"]["tree_jev_forward_tree_ms"] = round(tree_host_ms, 3)
+        result["boundary"]["tree_extra_pct"] = round((tree_host_ms / tree_ms - 1) * 100, 2)
+        result["boundary"]["tree_rows_equal_device_call"] = bool(np.array_equal(np.array(vh).reshape(nb, 2), v))
+        log(f"tree decision through jev_forward_tree: {tree_host_ms:.2f} ms ({(tree_host_ms / tree_ms - 1) * 100:+.1f} %)")
         # N1: the trunk's KV state (4096 positions, 872 MB) snapshotted and restored
         # inside HBM (the decider's question snapshot), against the host copy
         L.check(lib.jev_sync(h))
@@ -689,6 +731,29 @@ def main():
             gv = prof_read(lib, dh, L.PROF_GEMV)
             da = prof_read(lib, dh, L.PROF_DECODE_ATTN)
             L.check(lib.jev_profile_enable(dh, 0))
+        steps_ms = host_ms_tok = None
+        if not once:
+            # per-token latency (Benchmark.cs:411-422): the graph-replayed run
+            # with a timing event at every step boundary, and the reference's
+            # own loop -- one jev_forward of one token (host logits) plus the
+            # argmax on the host per step
+            L.check(lib.jev_profile_enable(dh, 2))
+            decode_run()
+            buf = np.empty(n_dec, np.float32)
+            got = ctypes.c_int32()
+            L.check(lib.jev_profile_steps(dh, buf.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n_dec,
+                                          ctypes.byref(got)))
+            L.check(lib.jev_profile_enable(dh, 0))
+            steps_ms = buf[:got.value]
+            L.check(lib.jev_kv_reset(dh))
+            dmodel.prefill(prompt)
+            nxt = int(prompt[-1])
+            host_ms_tok = []
+            for _ in range(n_dec):
+                t = time.perf_counter()
+                nxt = jev.index_of_max(dmodel.forward([nxt]))
+                host_ms_tok.append((time.perf_counter() - t) * 1e3)
+            host_ms_tok = np.array(host_ms_tok)
         gemv_gbs = gv[3] / (gv[1] * 1e-3) / 1e9 if gv[1] else 0.0
         log(f"Q5_1 decode: {ms_tok:.3f} ms/token ({1e3 / ms_tok:.1f} tok/s); GEMV {gemv_gbs:.0f} GB/s "
             f"({gv[1] / n_dec:.3f} ms/token of kernel time), attention {da[1] / n_dec:.3f} ms/token")
@@ -702,6 +767,15 @@ def main():
             "decode_attention_ms_per_token": round(da[1] / n_dec, 4),
             "first_tokens": [int(x) for x in toks[:8]],
         }
+        if steps_ms is not None:
+            result["decode_q5_1"]["graph_step_ms"] = {
+                "p50": round(float(np.median(steps_ms)), 4), "mean": round(float(np.mean(steps_ms)), 4),
+                "min": round(float(np.min(steps_ms)), 4), "max": round(float(np.max(steps_ms)), 4),
+                "steps": int(len(steps_ms))}
+            result["decode_q5_1"]["host_loop_ms"] = {
+                "p50": round(float(np.median(host_ms_tok)), 4), "mean": round(float(np.mean(host_ms_tok)), 4),
+                "what": "jev_forward of one token with host logits + argmax on the host, per step"}
+            log(f"decode step p50: graph {np.median(steps_ms):.3f} ms, host loop {np.median(host_ms_tok):.3f} ms")
         if not args.no_cpu:
             result["decode_q5_1"]["cpu_baseline"] = decode_cpu_baseline(jev, dsynth, dcfg, prompt, host)
         if not once:

@@ -174,8 +174,11 @@ int jev_forward_tree(jev_ctx *ctx, const int32_t *trunk, int32_t n_trunk, const 
 
 /* Greedy decode (Benchmark.cs:411-422 / ReasoningDecider.cs:157-178): feeds
  * `first`, then n_steps - 1 argmax tokens, one ForwardAsync([next]) each;
- * tokens_out receives the n_steps argmax ids (Kernels.ArgMax, lowest index on ties). */
-int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tokens_out);
+ * tokens_out (room for tokens_out_len ids) receives the n_steps argmax ids
+ * (Kernels.ArgMax, lowest index on ties).  A tokens_out shorter than n_steps
+ * is refused with JEV_EINVAL before any work, as the reference refuses a
+ * destination span that is too short (MinistralModel.cs:306). */
+int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tokens_out, size_t tokens_out_len);
 
 /* ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178, each step
  * a ForwardRowsAsync of one token per row, MinistralModel.cs:272-294, with the
@@ -184,7 +187,9 @@ int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tok
  * every step feeds each row's last token (first[r] at step 0) and takes each
  * row's argmax over the full vocabulary (lowest index on ties) as its next
  * token.  The step runs as a replayed HIP graph with the per-row state on the
- * device; tokens_out receives n_steps x n_rows ids, [step][row].  Every row
+ * device; tokens_out (room for tokens_out_len ids; fewer than n_steps x
+ * n_rows is JEV_EINVAL before any work) receives n_steps x n_rows ids,
+ * [step][row].  Every row
  * runs all n_steps: the caller ends a row at its stop token by discarding
  * what follows (rows are independent and the kernels batch-invariant, so a
  * row's tokens do not depend on which other rows run, as long as two or more
@@ -192,7 +197,8 @@ int jev_decode_greedy(jev_ctx *ctx, int32_t first, int32_t n_steps, int32_t *tok
  * rows' slots over the whole run must stay clear of the shared prefix and of
  * each other (JEV_EINVAL otherwise). */
 int jev_decode_rows_greedy(jev_ctx *ctx, int32_t shared, int32_t n_rows, const int32_t *row_base,
-                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out);
+                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out,
+                           size_t tokens_out_len);
 
 /* JevstralDecider.DecideAsync margins (:306-308) and softmax(z/T) (:310-313):
  * verdicts is n_options x (n_yes + n_no). */
@@ -220,11 +226,15 @@ int jev_sync(jev_ctx *ctx);
 /* The context's HIP stream (hipStream_t), for event timing by the caller. */
 void *jev_stream(jev_ctx *ctx);
 
-/* Kernel timing: with profiling enabled, the context records a HIP event pair
- * around every launch of the listed kernel classes on its own stream, and
- * accumulates launches, device time and algorithmic work (FLOPs of the
- * product, bytes of the weights and activations it must move).  Enabling
- * clears the counters; reading synchronises the stream. */
+/* Kernel timing: with profiling enabled (mode 1), the context records a HIP
+ * event pair around every launch of the listed kernel classes on its own
+ * stream, and accumulates launches, device time and algorithmic work (FLOPs of
+ * the product, bytes of the weights and activations it must move); the greedy
+ * decodes then launch kernel by kernel instead of replaying a graph.  Mode 2
+ * instead stamps only the step boundaries of the greedy decodes (graphs kept):
+ * jev_profile_steps returns the last decode's per-step device time in ms, the
+ * per-token latency Benchmark.cs:411-422 samples.  Mode 0 turns both off.
+ * Enabling clears the counters; reading synchronises the stream. */
 #define JEV_PROF_GEMM 0 /* MFMA prefill GEMM                     */
 #define JEV_PROF_ATTN 1 /* tree attention (prefill)              */
 #define JEV_PROF_GEMV 2 /* one-token quantized GEMV              */
@@ -233,6 +243,7 @@ void *jev_stream(jev_ctx *ctx);
 int jev_profile_enable(jev_ctx *ctx, int enable);
 int jev_profile_read(jev_ctx *ctx, int kernel_class, int64_t *launches, double *total_ms, double *flops,
                      double *bytes);
+int jev_profile_steps(jev_ctx *ctx, float *ms, int32_t n, int32_t *n_steps);
 
 /* ---- A single quantized weight resident in HBM ---- */
 

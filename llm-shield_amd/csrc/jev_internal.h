@@ -256,11 +256,15 @@ hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s);
 // Decode attention: one query token per entry, split over kDecodeKeys-key
 // chunks; leaves per-chunk partials for the consumer (GemvArgs::attn).
 constexpr int kDecodeKeys = 64;
-// Passes of single-token rows take the decode attention while their chunk
-// partials (rows x chunks of them) stay within this many.
+// A pass whose attention tiles are all single tokens (rows of one token each)
+// always takes the decode attention; its tokens are served in launch groups
+// whose chunk partials (tokens x chunks of them) stay within this many, so the
+// partials buffer stays bounded at any context.  The group size changes no
+// token's arithmetic.
 constexpr int kSingleRowsChunks = 4096;
 struct DecodeAttnArgs {
     int T = 0, n_heads = 0, group = 4, hd = 128, max_chunks = 0;
+    int t0 = 0; // first token of this launch: token t0 + blockIdx.x, partials at blockIdx.x
     const float *q = nullptr;
     const float *kc = nullptr, *vc = nullptr;
     int cap = 0;
@@ -268,7 +272,7 @@ struct DecodeAttnArgs {
     int start = 0; // causal append when the arrays are null
     const int32_t *start_dev = nullptr; // if set, the causal start is read from device memory
     float scale = 0.f;
-    float *part = nullptr;   // [T][heads][max_chunks][hd + 2]
+    float *part = nullptr;   // [T][heads][max_chunks][hd + 2], token t0 first
     // (T >= 2 needs the per-token arrays and q already rotated: rope_fused 0.)
     // One token (T = 1) with rope_fused: RoPE and the KV store happen here --
     // q from the projection partials of `rope` (q_in / k_in / v_in, nin,
@@ -288,7 +292,8 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s);
 // operand-tile layout the O projection's GEMM reads.
 struct AttnCombineArgs {
     int T = 0, n_heads = 0, max_chunks = 0;
-    const float *part = nullptr; // [T][heads][max_chunks][130]
+    int t0 = 0;                  // first token of this launch (as DecodeAttnArgs::t0)
+    const float *part = nullptr; // [T][heads][max_chunks][130], indexed from t0
     const int32_t *slot = nullptr, *shared_lo = nullptr, *shared_hi = nullptr, *segment = nullptr;
     uint16_t *ot = nullptr; // [T16][heads * 128] pair tiles
     float *xsum = nullptr;  // [T][heads * 4] block sums of ot (Q5_1 projections), or null

@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
     __shared__ __attribute__((aligned(16))) float qs[4][128];
     __shared__ float ps[4][kDecKeys];
     __shared__ float cs[64], sn[64]; // fused RoPE: cos / sin (times mscale) of the token's position
-    const int t = blockIdx.x, kvh = blockIdx.y, c = blockIdx.z;
+    const int tl = blockIdx.x, t = a.t0 + tl, kvh = blockIdx.y, c = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qdim = a.n_heads * 128;
     const int start = a.start_dev ? *a.start_dev : a.start;
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
                 make_float4(ok ? v4.x : 0.f, ok ? v4.y : 0.f, ok ? v4.z : 0.f, ok ? v4.w : 0.f);
         }
     }
-    float *part_base = a.part + ((size_t)t * a.n_heads) * a.max_chunks * 130;
+    float *part_base = a.part + ((size_t)tl * a.n_heads) * a.max_chunks * 130;
     for (int h0 = 0; h0 < a.group; h0 += 4) { // every wave takes every barrier
         const int h = h0 + wave;
         const bool active = h < a.group;
@@ -661,10 +661,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecodeAttnArgs a)
 hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    // several tokens: each its own layout entry (and position, when RoPE is
-    // fused: the caller guarantees no token sees another's new key)
-    if (a.T > 1 && (!a.slot || !a.shared_lo || !a.shared_hi || !a.segment || (a.rope_fused && !a.rope.pos)))
+    // several tokens (or a later group of them): each its own layout entry
+    // (and position, when RoPE is fused: the caller guarantees no token sees
+    // another's new key)
+    if ((a.T > 1 || a.t0 > 0) && (!a.slot || !a.shared_lo || !a.shared_hi || !a.segment || (a.rope_fused && !a.rope.pos)))
         return hipErrorInvalidValue;
+    if (a.t0 < 0) return hipErrorInvalidValue;
     if (a.hd != 128 || a.group < 1 || a.n_heads % a.group != 0) return hipErrorInvalidValue;
     if (!a.rope.q_in || !a.rope.k_in || !a.rope.v_in || !a.rope.freqs || a.rope.nin < 1) return hipErrorInvalidValue;
     if (a.rope_fused && (a.rope.hd != 128 || a.rope.half > 64 || a.rope.nin < 1 || !a.rope.q_in ||
@@ -685,11 +687,11 @@ hipError_t launch_attn_decode(const DecodeAttnArgs &a, hipStream_t s)
 // context as the fp16 pair (hi rounded to nearest, lo the remainder).
 __global__ __launch_bounds__(64) void attn_combine_kernel(AttnCombineArgs a)
 {
-    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int tl = blockIdx.x, t = a.t0 + tl, h = blockIdx.y, lane = threadIdx.x;
     const int slot = a.slot[t], slo = a.shared_lo[t], shi = a.shared_hi[t], seg = a.segment[t];
     const int limit = (shi - slo) + (slot - seg + 1);
     const int nch = min((limit + kDecodeKeys - 1) / kDecodeKeys, a.max_chunks);
-    const float *pp = a.part + ((size_t)t * a.n_heads + h) * a.max_chunks * 130;
+    const float *pp = a.part + ((size_t)tl * a.n_heads + h) * a.max_chunks * 130;
     float M = -INFINITY, L = 0.f, v0 = 0.f, v1 = 0.f;
     for (int c0 = 0; c0 < nch; c0 += 8) {
         float mv[8], lv[8];
@@ -742,7 +744,8 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnCombineArgs a)
 hipError_t launch_attn_combine(const AttnCombineArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
-    if (a.n_heads < 1 || a.max_chunks < 1 || !a.part || !a.ot || !a.slot || !a.shared_lo || !a.shared_hi || !a.segment)
+    if (a.t0 < 0 || a.n_heads < 1 || a.max_chunks < 1 || !a.part || !a.ot || !a.slot || !a.shared_lo || !a.shared_hi ||
+        !a.segment)
         return hipErrorInvalidValue;
     launch_stamped(a.ev_start, a.ev_stop, attn_combine_kernel, dim3(a.T, a.n_heads), dim3(64), 0, s, a);
     return hipGetLastError();

@@ -151,6 +151,11 @@ struct jev_ctx {
     };
     bool profiling = false;
     bool capturing = false; // a graph capture is open on the stream (no event records)
+    // Step stamps (jev_profile_enable mode 2): the greedy decodes keep their
+    // graphs and record a timing event at every step boundary.
+    bool step_stamps = false;
+    std::vector<hipEvent_t> step_ev;
+    std::vector<float> step_ms; // the last greedy decode's per-step device times
     std::vector<hipEvent_t> ev_pool;
     size_t ev_used = 0;
     std::vector<ProfRec> prof;
@@ -266,6 +271,26 @@ struct CallScope {
     ~CallScope() { c->active.store(0); }
     bool cancelled() const { return c->cancel_id.load() == id; }
 };
+
+// Timing events for the step boundaries of a greedy decode of n steps.
+int step_events(jev_ctx *c, int n)
+{
+    while ((int)c->step_ev.size() < n + 1) {
+        hipEvent_t e = nullptr;
+        HIP_TRY(hipEventCreate(&e));
+        c->step_ev.push_back(e);
+    }
+    c->step_ms.clear();
+    return JEV_OK;
+}
+
+// After the stream has drained: the device time of each of the `launched` steps.
+void read_step_times(jev_ctx *c, int launched)
+{
+    c->step_ms.assign(launched, 0.f);
+    for (int i = 0; i < launched; i++)
+        if (hipEventElapsedTime(&c->step_ms[i], c->step_ev[i], c->step_ev[i + 1]) != hipSuccess) c->step_ms[i] = -1.f;
+}
 
 double weight_bytes(const QWeight &w) { return (double)row_bytes(w.type, w.cols) * w.rows; }
 
@@ -411,6 +436,10 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     return JEV_OK;
 }
 
+// Tokens per decode-attention launch of a single-token-rows pass: the chunk
+// partials of one launch stay within kSingleRowsChunks.
+int single_rows_group(int T, int max_chunks) { return std::max(1, std::min(T, kSingleRowsChunks / std::max(1, max_chunks))); }
+
 int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks, bool single_rows = false)
 {
     const jev_config &f = c->cfg;
@@ -430,7 +459,8 @@ int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks, boo
         HIP_TRY(c->f32.ensure((size_t)2 * f.ffn));
         HIP_TRY(c->part.ensure((size_t)f.n_heads * std::max(1, max_chunks) * 130));
     } else {
-        if (single_rows) HIP_TRY(c->part.ensure((size_t)T * f.n_heads * std::max(1, max_chunks) * 130));
+        if (single_rows)
+            HIP_TRY(c->part.ensure((size_t)single_rows_group(T, max_chunks) * f.n_heads * std::max(1, max_chunks) * 130));
         size_t T16 = ((size_t)T + 15) & ~(size_t)15;
         HIP_TRY(c->xt.ensure(T16 * std::max(f.hidden, c->qdim()) * 2));
         HIP_TRY(c->ft.ensure(T16 * f.ffn * 2));
@@ -559,7 +589,10 @@ int build_plan(jev_ctx *c, const int32_t *tokens, bool tokens_on_device, int T, 
     p.n_tiles = (int)tiles.size();
     p.kv_rows = std::min<double>(p.end, max_limit + (double)T);
     p.max_chunks = (max_limit + kDecodeKeys - 1) / kDecodeKeys;
-    p.single_rows = L && T >= 2 && p.n_tiles == T && (long)T * std::max(1, p.max_chunks) <= kSingleRowsChunks;
+    // a function of the layout's shape alone -- not of the context length or
+    // of how many rows run -- so a rows step takes the same attention kernel
+    // whether it is replayed from a graph or run step by step
+    p.single_rows = L && T >= 2 && p.n_tiles == T;
     if (p.single_rows) {
         std::vector<int32_t> fresh(L->slot, L->slot + T);
         std::sort(fresh.begin(), fresh.end());
@@ -887,15 +920,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             da.part = c->part.p;
             da.rope_fused = rows_fused ? 1 : 0;
             da.rope = ra;
-            {
-                ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs,
-                             8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs, true);
-                da.ev_start = ps.a;
-                da.ev_stop = ps.z;
-                HIP_TRY(launch_attn_decode(da, s));
-            }
             AttnCombineArgs ca;
-            ca.T = T;
             ca.n_heads = f.n_heads;
             ca.max_chunks = p.max_chunks;
             ca.part = c->part.p;
@@ -905,7 +930,20 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             ca.segment = p.d_seg;
             ca.ot = c->xt.p;
             ca.xsum = L.o.type == kQ5_1 ? c->xsum.p : nullptr;
-            HIP_TRY(launch_attn_combine(ca, s));
+            // token groups share the partials buffer, one after the other
+            const int G = single_rows_group(T, p.max_chunks);
+            for (int t0 = 0; t0 < T; t0 += G) {
+                da.t0 = ca.t0 = t0;
+                da.T = ca.T = std::min(G, T - t0);
+                {
+                    ProfScope ps(c, JEV_PROF_DECODE_ATTN, 4.0 * f.head_dim * f.n_heads * p.visible_pairs * da.T / T,
+                                 8.0 * f.head_dim * f.n_kv_heads * p.visible_pairs * da.T / T, true);
+                    da.ev_start = ps.a;
+                    da.ev_stop = ps.z;
+                    HIP_TRY(launch_attn_decode(da, s));
+                }
+                HIP_TRY(launch_attn_combine(ca, s));
+            }
             CAP_TRY(cap_pair(c, cap, layer_tap(l, "attn_weighted"), c->xt.p, T, qdim));
         } else {
             AttnArgs aa;
@@ -1225,6 +1263,7 @@ void jev_destroy(jev_ctx *c)
     for (auto e : c->layer_ev)
         if (e) (void)hipEventDestroy(e);
     for (auto e : c->ev_pool) (void)hipEventDestroy(e);
+    for (auto e : c->step_ev) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1440,9 +1479,9 @@ int jev_kv_snapshot_device(jev_ctx *c, int32_t length, jev_snapshot **out)
     sn->floats = 2 * (size_t)f.n_layers * f.n_kv_heads * length * f.head_dim;
     hipError_t e = hipMalloc((void **)&sn->data, std::max<size_t>(sn->floats, 1) * sizeof(float));
     if (e != hipSuccess) {
+        const size_t bytes = sn->floats * sizeof(float);
         delete sn;
-        return fail(JEV_ENOMEM, "device snapshot of %d positions (%zu bytes): %s", length, sn->floats * 4,
-                    hipGetErrorString(e));
+        return fail(JEV_ENOMEM, "device snapshot of %d positions (%zu bytes): %s", length, bytes, hipGetErrorString(e));
     }
     int rc = kv_flat_copy(c, length, sn->data, true, hipMemcpyDeviceToDevice);
     if (!rc && (e = hipStreamSynchronize(c->stream)) != hipSuccess) rc = fail(JEV_EDEVICE, "snapshot: %s", hipGetErrorString(e));
@@ -1614,11 +1653,15 @@ int jev_forward_tree(jev_ctx *c, const int32_t *trunk, int32_t n_trunk, const in
     return jev_forward(c, tokens.data(), total, &L, JEV_OUT_SELECTED, rows, n_rows, out, out_len);
 }
 
-int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *tokens_out)
+int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *tokens_out, size_t tokens_out_len)
 {
+    // the destination is checked before anything else, as the reference
+    // checks its spans on entry (MinistralModel.cs:306)
+    if (n_steps <= 0 || !tokens_out) return fail(JEV_EINVAL, "bad arguments");
+    if (tokens_out_len < (size_t)n_steps)
+        return fail(JEV_EINVAL, "tokens_out holds %zu ids; %d steps need %d.", tokens_out_len, n_steps, n_steps);
     int rc = check_ready(c);
     if (rc) return rc;
-    if (n_steps <= 0 || !tokens_out) return fail(JEV_EINVAL, "bad arguments");
     if (first < 0 || first >= c->embd.rows) return fail(JEV_EINVAL, "Token id %d is outside the embedding table.", first);
     CallScope call(c);
     // Every step is the same launch sequence: the token, the cache length and
@@ -1660,6 +1703,12 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
     }
     // Steps are enqueued at most kLeadLayers ahead of the device (one event
     // per step), so a cancel stops the loop within that many steps.
+    const bool stamps = c->step_stamps && !c->profiling;
+    if (!rc && stamps) rc = step_events(c, n_steps);
+    if (!rc && stamps) {
+        hipError_t e = hipEventRecord(c->step_ev[0], c->stream);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+    }
     int launched = 0;
     while (!rc && launched < n_steps) {
         if (launched >= jev_ctx::kLeadLayers) {
@@ -1685,12 +1734,14 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
         }
         launched++;
         hipError_t e = hipEventRecord(c->layer_ev[(launched - 1) % jev_ctx::kLayerEvents], c->stream);
+        if (e == hipSuccess && stamps) e = hipEventRecord(c->step_ev[launched], c->stream);
         if (e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
     }
     hipError_t e = hipStreamSynchronize(c->stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "decode: %s", hipGetErrorString(e));
+    if (!rc && stamps) read_step_times(c, launched);
     if (!rc && call.cancelled()) rc = fail(JEV_ECANCELED, "greedy decoding was cancelled after %d steps", launched);
     // every launched step ran to the end and advanced the cache by one token
     if (!rc || rc == JEV_ECANCELED) c->len = std::max(c->len, start + launched);
@@ -1707,12 +1758,16 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
 // attention tiles live in the plan's device buffers and rows_step_kernel
 // advances them, so nothing returns to the host between steps.
 int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int32_t *row_base,
-                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out)
+                           const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out,
+                           size_t tokens_out_len)
 {
-    int rc = check_ready(c);
-    if (rc) return rc;
     if (n_rows <= 0 || n_steps <= 0 || shared < 0 || !row_base || !row_length || !first || !tokens_out)
         return fail(JEV_EINVAL, "bad arguments");
+    if (tokens_out_len < (size_t)n_steps * (size_t)n_rows)
+        return fail(JEV_EINVAL, "tokens_out holds %zu ids; %d steps of %d rows need %zu.", tokens_out_len, n_steps,
+                    n_rows, (size_t)n_steps * (size_t)n_rows);
+    int rc = check_ready(c);
+    if (rc) return rc;
     // every row's slots over the whole run, [base, base + length + steps),
     // clear of the shared prefix and of each other
     std::vector<std::pair<int64_t, int64_t>> span(n_rows);
@@ -1758,7 +1813,11 @@ int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int
     HIP_TRY(c->dec_state.ensure((size_t)n_rows * (n_steps + 1)));
     int32_t *rowstep = c->dec_state.p, *out = c->dec_state.p + n_rows;
     HIP_TRY(hipMemsetAsync(rowstep, 0, (size_t)n_rows * sizeof(int32_t), c->stream));
-    AttnTile *tiles = n_rows >= 2 ? c->tiles.p : nullptr;
+    // two or more rows: every row is its own attention tile (the rows' slots
+    // never meet), so the step takes the decode attention per token, whose
+    // layout arrays rows_step_kernel advances; no attention tile is replayed
+    if (n_rows >= 2 && !p.single_rows) return fail(JEV_EINVAL, "the rows do not form one-token attention tiles");
+    AttnTile *tiles = nullptr;
     auto step = [&]() -> int {
         int r = enqueue_forward(c, p, JEV_OUT_FULL, 0, c->logits.p);
         if (r) return r;
@@ -1778,6 +1837,12 @@ int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int
         if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "graph capture: %s", hipGetErrorString(e));
         if (!rc && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
             rc = fail(JEV_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
+    }
+    const bool stamps = c->step_stamps && !c->profiling;
+    if (!rc && stamps) rc = step_events(c, n_steps);
+    if (!rc && stamps) {
+        hipError_t e = hipEventRecord(c->step_ev[0], c->stream);
+        if (e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
     }
     int launched = 0;
     while (!rc && launched < n_steps) {
@@ -1804,12 +1869,14 @@ int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int
         }
         launched++;
         hipError_t e = hipEventRecord(c->layer_ev[(launched - 1) % jev_ctx::kLayerEvents], c->stream);
+        if (e == hipSuccess && stamps) e = hipEventRecord(c->step_ev[launched], c->stream);
         if (e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
     }
     hipError_t e = hipStreamSynchronize(c->stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (!rc && e != hipSuccess) rc = fail(JEV_EDEVICE, "rows decode: %s", hipGetErrorString(e));
+    if (!rc && stamps) read_step_times(c, launched);
     if (!rc && call.cancelled()) rc = fail(JEV_ECANCELED, "rows decoding was cancelled after %d steps", launched);
     if (!rc || rc == JEV_ECANCELED) {
         int32_t end = shared; // KvCache.Advance to the highest slot written
@@ -1856,10 +1923,21 @@ int jev_margins(const float *v, int32_t n_options, int32_t n_yes, int32_t n_no, 
 int jev_profile_enable(jev_ctx *c, int enable)
 {
     if (!c) return fail(JEV_EINVAL, "null context");
+    if (enable < 0 || enable > 2) return fail(JEV_EINVAL, "profiling mode %d is not 0, 1 or 2", enable);
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->prof.clear();
     c->ev_used = 0;
-    c->profiling = enable != 0;
+    c->profiling = enable == 1;
+    c->step_stamps = enable == 2;
+    c->step_ms.clear();
+    return JEV_OK;
+}
+
+int jev_profile_steps(jev_ctx *c, float *ms, int32_t n, int32_t *n_steps)
+{
+    if (!c || !n_steps || n < 0 || (n > 0 && !ms)) return fail(JEV_EINVAL, "bad arguments");
+    *n_steps = (int32_t)c->step_ms.size();
+    std::copy_n(c->step_ms.begin(), std::min<size_t>((size_t)n, c->step_ms.size()), ms);
     return JEV_OK;
 }
 

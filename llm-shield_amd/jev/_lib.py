@@ -114,8 +114,8 @@ def lib():
         "jev_forward": (c_int, [c_void_p, I32P, c_int32, POINTER(Layout), c_int, I32P, c_int32, F32P, c_size_t]),
         "jev_forward_tree": (c_int, [c_void_p, I32P, c_int32, I32P, I32P, c_int32, I32P, c_int32, F32P, c_size_t]),
         "jev_capture": (c_int, [c_void_p, I32P, c_int32, SINK, c_void_p, F32P, c_size_t]),
-        "jev_decode_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P]),
-        "jev_decode_rows_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P, I32P, I32P, c_int32, I32P]),
+        "jev_decode_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P, c_size_t]),
+        "jev_decode_rows_greedy": (c_int, [c_void_p, c_int32, c_int32, I32P, I32P, I32P, c_int32, I32P, c_size_t]),
         "jev_margins": (c_int, [F32P, c_int32, c_int32, c_int32, c_float, F32P, F32P]),
         "jev_cancel": (None, [c_void_p]),
         "jev_forward_device": (c_int, [c_void_p, c_void_p, c_int32, POINTER(Layout), c_int, I32P, c_int32, c_void_p]),
@@ -124,6 +124,7 @@ def lib():
         "jev_profile_enable": (c_int, [c_void_p, c_int]),
         "jev_profile_read": (c_int, [c_void_p, c_int, POINTER(c_int64), POINTER(ctypes.c_double),
                                      POINTER(ctypes.c_double), POINTER(ctypes.c_double)]),
+        "jev_profile_steps": (c_int, [c_void_p, F32P, c_int32, I32P]),
         "jev_weight_create": (c_int, [c_int, c_int64, c_int64, c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
         "jev_weight_destroy": (None, [c_void_p]),
         "jev_matmul_device": (c_int, [c_void_p, c_void_p, c_int32, c_void_p]),
@@ -157,7 +158,7 @@ EXPORTED = [
     "jev_last_error", "jev_create", "jev_destroy", "jev_bind_tensor", "jev_finalize", "jev_kv_length",
     "jev_kv_capacity", "jev_kv_reserve", "jev_kv_truncate", "jev_kv_reset", "jev_kv_snapshot", "jev_kv_restore",
     "jev_forward", "jev_forward_tree", "jev_decode_greedy", "jev_decode_rows_greedy", "jev_margins", "jev_cancel", "jev_forward_device",
-    "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_weight_create", "jev_weight_destroy",
+    "jev_sync", "jev_stream", "jev_profile_enable", "jev_profile_read", "jev_profile_steps", "jev_weight_create", "jev_weight_destroy",
     "jev_matmul_device", "jev_weight_sync", "jev_dequantize", "jev_matmul_q", "jev_quantize", "jev_synth_tensor",
     "jev_set_matmul_strategy", "jev_get_matmul_strategy", "jev_quantize_activations", "jev_rope_table",
     "jev_matmul_device_noalloc", "jev_capture", "jev_weight_stream", "jev_kv_snapshot_device",

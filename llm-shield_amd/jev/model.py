@@ -381,7 +381,7 @@ class MinistralModel:
     def decode_greedy(self, first: int, steps: int) -> np.ndarray:
         """Greedy decode: ForwardAsync([next]) + ArgMax per step (Benchmark.cs:411-422)."""
         out = np.empty(steps, np.int32)
-        L.check(self._lib.jev_decode_greedy(self._h, first, steps, _ptr(out, ctypes.c_int32)))
+        L.check(self._lib.jev_decode_greedy(self._h, first, steps, _ptr(out, ctypes.c_int32), out.size))
         return out
 
     def decode_rows_greedy(self, shared: int, row_base, row_length, first, steps: int) -> np.ndarray:
@@ -395,7 +395,7 @@ class MinistralModel:
         out = np.empty((steps, n), np.int32)
         L.check(self._lib.jev_decode_rows_greedy(self._h, shared, n, _ptr(base, ctypes.c_int32),
                                                  _ptr(length, ctypes.c_int32), _ptr(fst, ctypes.c_int32), steps,
-                                                 _ptr(out, ctypes.c_int32)))
+                                                 _ptr(out, ctypes.c_int32), out.size))
         return out
 
     def forward_capture(self, tokens):

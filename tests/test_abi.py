@@ -62,3 +62,22 @@ def test_layout_helpers_follow_the_reference():
     assert list(t.position) == [5, 6, 7, 8, 9, 8, 9, 10] and list(t.outputs) == [4, 7] and t.end == 13
     r = jev.TokenLayout.rows(4, [10, 20], [2, 0], [1, 3])
     assert list(r.slot) == [12, 20, 21, 22] and r.end == 23
+
+
+def test_greedy_decodes_refuse_a_short_destination_before_any_work():
+    # The destination length is checked on entry, before the context is
+    # touched (no device is involved: the context here is null).
+    L = jev.lib()
+    out = np.zeros(7, np.int32)
+    p = out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    assert L.jev_decode_greedy(None, 1, 8, p, out.size) == jev._lib.JEV_EINVAL
+    assert b"holds 7 ids; 8 steps need 8" in L.jev_last_error()
+    rows = np.zeros(3, np.int32)
+    rp = rows.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    assert L.jev_decode_rows_greedy(None, 0, 3, rp, rp, rp, 3, p, out.size) == jev._lib.JEV_EINVAL
+    assert b"holds 7 ids; 3 steps of 3 rows need 9" in L.jev_last_error()
+    # long enough: the next check is the context's
+    big = np.zeros(9, np.int32)
+    bp = big.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    assert L.jev_decode_rows_greedy(None, 0, 3, rp, rp, rp, 3, bp, big.size) == jev._lib.JEV_EINVAL
+    assert b"null context" in L.jev_last_error()

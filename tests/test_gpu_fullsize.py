@@ -3,7 +3,8 @@ vocabulary 131072, synthetic Q8_0 weights (counter-based N(0, 0.02), the
 ggml quantizer) -- the model every benchmark row runs.
 
 * a short prompt and two decode steps against the oracle at the logits bar
-  (Numeric.Close <= 1e-3);
+  (Numeric.Close <= 1e-3), and the benchmark's 256-token prefill (seed 11)
+  with its full-vocabulary logits;
 * the reference's bitwise contracts at full size: the tree pass equals each
   branch run alone after the trunk and the branches off a cached trunk
   (DeciderTests.cs:55-91, with the benchmark tree's 9 x 48-token branches),
@@ -53,6 +54,23 @@ def test_full_shape_logits_and_decode_match_oracle(model, synth):
             assert worst_close(ref.forward([t]), model.forward([t])) <= 1e-3
     finally:
         ref.close()
+
+
+def test_headline_prefill_logits_match_oracle(model, synth):
+    # the benchmark's own workload: 256 uniform token ids (seed 11) through the
+    # Q8_0 3B shape, final-position logits over the whole vocabulary
+    # (MinistralModel.cs:411-424), at the logits bar (Numeric.Close <= 1e-3)
+    tokens = jev.random_tokens(256, VOCAB, 11)
+    model.reset_kv_cache()
+    g = model.forward(tokens)
+    oracle.set_threads(max(1, min(16, os.cpu_count() or 1)))
+    ref = oracle.OracleModel(synth.config).bind_synth(synth)
+    try:
+        e = ref.forward(tokens)
+    finally:
+        ref.close()
+    assert g.shape == (VOCAB,)
+    assert worst_close(e, g) <= 1e-3
 
 
 def test_full_shape_tree_equals_branches_alone_bitwise(model):

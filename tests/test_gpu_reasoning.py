@@ -122,3 +122,67 @@ def test_rows_graph_rejects_rows_that_meet(gpu, synth):
         with pytest.raises(jev.ArgumentError):
             m.decode_rows_greedy(8, [10, 40], [0, 0], [1, 5000], 4)  # outside the embedding table
         assert m.cached_token_count == n
+
+
+def test_rows_over_a_long_prefix_run_in_token_groups_and_match_the_loop(gpu, synth):
+    # 12 rows over a 22000-token shared prefix: 12 x 345 chunk partials exceed
+    # one decode-attention launch's budget (4096), so every step runs the rows
+    # in two token groups.  The graph (kernel choice fixed at capture) must
+    # give the tokens of the step-by-step loop in which rows stop one after
+    # another, and a row's tokens must not depend on the rows beside it (the
+    # same row decoded in a pair, one launch group).
+    trunk = jev.random_tokens(22000, 2048, 91)
+    n_rows, steps = 12, 6
+    prompts = [list(jev.random_tokens(3 + r, 2048, 92 + r)) for r in range(n_rows)]
+    bases = [22016 + 64 * r for r in range(n_rows)]
+    with synth.open(0) as m:
+        def start(rows):
+            m.reset_kv_cache()
+            m.prefill(trunk)
+            logits = m.forward_rows(len(trunk), [bases[r] for r in rows], [0] * len(rows), [prompts[r] for r in rows])
+            return [jev.reasoning.index_of_max(z) for z in logits]
+
+        first = start(range(n_rows))
+        g = m.decode_rows_greedy(len(trunk), bases, [len(p) for p in prompts], first, steps)
+        # step by step, rows 0..4 stopping after 1..5 steps
+        assert start(range(n_rows)) == first
+        lengths = [len(p) for p in prompts]
+        live, nxt = list(range(n_rows)), list(first)
+        loop = {r: [] for r in range(n_rows)}
+        for step in range(steps):
+            logits = m.forward_rows(len(trunk), [bases[r] for r in live], [lengths[r] for r in live],
+                                    [[nxt[r]] for r in live])
+            for r, z in zip(live, logits):
+                lengths[r] += 1
+                nxt[r] = jev.reasoning.index_of_max(z)
+                loop[r].append(nxt[r])
+            live = [r for r in live if not (r < 5 and len(loop[r]) == r + 1)]
+            if len(live) < 2:
+                break
+        for r in range(n_rows):
+            assert list(g[:len(loop[r]), r]) == loop[r], r
+        # rows 3 and 9 alone as a pair
+        pair = start([3, 9])
+        assert pair == [first[3], first[9]]
+        gp = m.decode_rows_greedy(len(trunk), [bases[3], bases[9]], [len(prompts[3]), len(prompts[9])], pair, steps)
+    assert np.array_equal(gp[:, 0], g[:, 3]) and np.array_equal(gp[:, 1], g[:, 9])
+
+
+def test_greedy_decodes_refuse_a_short_destination(gpu, synth):
+    import ctypes
+    with synth.open(0) as m:
+        m.reset_kv_cache()
+        m.prefill(jev.random_tokens(8, 2048, 93))
+        n = m.cached_token_count
+        L = jev.lib()
+        out = np.zeros(5, np.int32)
+        p = out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        assert L.jev_decode_greedy(m._h, 1, 6, p, out.size) == jev._lib.JEV_EINVAL
+        rows = np.array([16, 32], np.int32)
+        lens = np.zeros(2, np.int32)
+        first = np.array([1, 2], np.int32)
+        i32 = ctypes.POINTER(ctypes.c_int32)
+        assert L.jev_decode_rows_greedy(m._h, 8, 2, rows.ctypes.data_as(i32), lens.ctypes.data_as(i32),
+                                        first.ctypes.data_as(i32), 3, p, out.size) == jev._lib.JEV_EINVAL
+        assert m.cached_token_count == n
+        assert np.all(out == 0)
