@@ -550,10 +550,27 @@ def main():
     for _ in range(args.steps):
         host_step()
     host_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    # the same synchronous shape without the throttle: the device-buffer call,
+    # then the logits copied to the host and the stream drained, per call
+    h_copy = torch.empty(cfg.vocab, dtype=torch.float32)
+
+    def sync_step():
+        step()
+        L.check(lib.jev_sync(h))
+        h_copy.copy_(d_out)  # blocking device-to-host copy
+
+    for _ in range(max(1, args.warmup)):
+        sync_step()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sync_step()
+    sync_ms = (time.perf_counter() - t0) / args.steps * 1e3
     log(f"prefill through jev_forward (host buffers, throttled): {host_ms:.3f} ms/step "
-        f"({(host_ms / ms_step - 1) * 100:+.1f} % against the device-buffer call)")
+        f"({(host_ms / ms_step - 1) * 100:+.1f} % against the device-buffer call; "
+        f"{sync_ms:.3f} ms for that call made synchronous with its logits copied out, no throttle)")
     boundary = {"prefill_jev_forward_ms": round(host_ms, 4), "prefill_jev_forward_tok_s": round(T / host_ms * 1e3, 1),
                 "prefill_extra_pct": round((host_ms / ms_step - 1) * 100, 2),
+                "prefill_device_call_synchronous_ms": round(sync_ms, 4),
                 "logits_equal_device_call": bool(np.array_equal(h_logits, gpu_logits))}
 
     gemm_avg_ms = gemm[1] / max(gemm[0], 1)
