@@ -320,10 +320,9 @@ hipError_t launch_argmax_decode(const float *x, int n, float *sv, int32_t *si, i
 hipError_t launch_argmax(const float *x, int n, int32_t *result, float *scratch_val, int32_t *scratch_idx,
                          hipStream_t s);
 // Greedy step of the rows layout: per row, argmax(logits[r]) -> tokens[r] and
-// out[rowstep[r] * n_rows + r]; slot[r], pos[r], tiles[r].slot0 and
-// rowstep[r] advance by one (tiles may be null).
+// out[rowstep[r] * n_rows + r]; slot[r], pos[r] and rowstep[r] advance by one.
 hipError_t launch_rows_step(const float *logits, int vocab, int n_rows, int32_t *tokens, int32_t *slot, int32_t *pos,
-                            AttnTile *tiles, int32_t *rowstep, int32_t *out, hipStream_t s);
+                            int32_t *rowstep, int32_t *out, hipStream_t s);
 
 // KV copy for capacity growth: [L*kvh] heads of `len` rows from stride old_cap to new_cap.
 // Pair shadow of a fp32 cache: [heads_total][cap][hd] -> [heads_total][cap][hi, lo][hd]

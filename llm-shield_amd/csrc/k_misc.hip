@@ -500,11 +500,10 @@ hipError_t launch_argmax_decode(const float *x, int n, float *sv, int32_t *si, i
 // One greedy step of the rows layout (ReasoningDecider.cs:157-178): row r's
 // argmax over its logits (lowest index on ties, Kernels.ArgMax) becomes its
 // next input token and is recorded at out[rowstep[r] * n_rows + r]; the
-// row's cache slot, position and attention tile (one token each) advance by
-// one.  Each workgroup owns one row, so no two touch the same state.
+// row's cache slot and position advance by one.  Each workgroup owns one row,
+// so no two touch the same state.
 __global__ __launch_bounds__(256) void rows_step_kernel(const float *logits, int vocab, int n_rows, int32_t *tokens,
-                                                       int32_t *slot, int32_t *pos, AttnTile *tiles, int32_t *rowstep,
-                                                       int32_t *out)
+                                                       int32_t *slot, int32_t *pos, int32_t *rowstep, int32_t *out)
 {
     __shared__ float bv[256];
     __shared__ int bi[256];
@@ -533,16 +532,15 @@ __global__ __launch_bounds__(256) void rows_step_kernel(const float *logits, int
         rowstep[r] = rowstep[r] + 1;
         slot[r] = slot[r] + 1;
         pos[r] = pos[r] + 1;
-        if (tiles) tiles[r].slot0 = tiles[r].slot0 + 1;
     }
 }
 
 hipError_t launch_rows_step(const float *logits, int vocab, int n_rows, int32_t *tokens, int32_t *slot, int32_t *pos,
-                            AttnTile *tiles, int32_t *rowstep, int32_t *out, hipStream_t s)
+                            int32_t *rowstep, int32_t *out, hipStream_t s)
 {
     if (n_rows <= 0 || vocab <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rows_step_kernel, dim3(n_rows), dim3(256), 0, s, logits, vocab, n_rows, tokens, slot, pos, tiles,
-                       rowstep, out);
+    hipLaunchKernelGGL(rows_step_kernel, dim3(n_rows), dim3(256), 0, s, logits, vocab, n_rows, tokens, slot, pos, rowstep,
+                       out);
     return hipGetLastError();
 }
 

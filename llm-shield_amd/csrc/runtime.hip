@@ -1754,9 +1754,9 @@ int jev_decode_greedy(jev_ctx *c, int32_t first, int32_t n_steps, int32_t *token
 
 // ReasoningDecider's batched greedy loop (ReasoningDecider.cs:157-178 through
 // ForwardRowsAsync, MinistralModel.cs:272-294): the rows-layout step captured
-// as a HIP graph and replayed.  The per-row tokens, slots, positions and
-// attention tiles live in the plan's device buffers and rows_step_kernel
-// advances them, so nothing returns to the host between steps.
+// as a HIP graph and replayed.  The per-row tokens, slots and positions live
+// in the plan's device buffers and rows_step_kernel advances them, so nothing
+// returns to the host between steps.
 int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int32_t *row_base,
                            const int32_t *row_length, const int32_t *first, int32_t n_steps, int32_t *tokens_out,
                            size_t tokens_out_len)
@@ -1817,13 +1817,12 @@ int jev_decode_rows_greedy(jev_ctx *c, int32_t shared, int32_t n_rows, const int
     // never meet), so the step takes the decode attention per token, whose
     // layout arrays rows_step_kernel advances; no attention tile is replayed
     if (n_rows >= 2 && !p.single_rows) return fail(JEV_EINVAL, "the rows do not form one-token attention tiles");
-    AttnTile *tiles = nullptr;
     auto step = [&]() -> int {
         int r = enqueue_forward(c, p, JEV_OUT_FULL, 0, c->logits.p);
         if (r) return r;
         hipError_t e = launch_rows_step(c->logits.p, c->cfg.vocab, n_rows, const_cast<int32_t *>(p.d_tokens),
-                                        const_cast<int32_t *>(p.d_slot), const_cast<int32_t *>(p.d_pos), tiles, rowstep,
-                                        out, c->stream);
+                                        const_cast<int32_t *>(p.d_slot), const_cast<int32_t *>(p.d_pos), rowstep, out,
+                                        c->stream);
         return e == hipSuccess ? JEV_OK : fail(JEV_EDEVICE, "rows step: %s", hipGetErrorString(e));
     };
     hipGraph_t graph = nullptr;

@@ -186,3 +186,27 @@ def test_greedy_decodes_refuse_a_short_destination(gpu, synth):
                                         first.ctypes.data_as(i32), 3, p, out.size) == jev._lib.JEV_EINVAL
         assert m.cached_token_count == n
         assert np.all(out == 0)
+
+
+def test_step_stamps_time_every_step_and_change_no_token(gpu, synth):
+    # jev_profile_enable mode 2: a timing event at every step boundary of a
+    # greedy decode, the graphs kept; the tokens are those of the plain run
+    import ctypes
+    tokens = jev.random_tokens(40, 2048, 94)
+    L = jev.lib()
+    with synth.open(0) as m:
+        m.reset_kv_cache()
+        m.prefill(tokens)
+        want = m.decode_greedy(int(tokens[-1]), 7)
+        m.reset_kv_cache()
+        m.prefill(tokens)
+        jev._lib.check(L.jev_profile_enable(m._h, 2))
+        got = m.decode_greedy(int(tokens[-1]), 7)
+        ms = np.zeros(16, np.float32)
+        n = ctypes.c_int32()
+        jev._lib.check(L.jev_profile_steps(m._h, ms.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ms.size,
+                                           ctypes.byref(n)))
+        jev._lib.check(L.jev_profile_enable(m._h, 0))
+    assert np.array_equal(got, want)
+    assert n.value == 7
+    assert np.all(ms[:7] > 0) and np.all(ms[7:] == 0)
