@@ -90,6 +90,12 @@ struct GemmArgs {
     int ldy = 0;
     float *y = nullptr;
     int ksplit = 1;                      // store mode: K in ksplit ranges, partial z at y + z*M*ldy
+    // fold (store mode, ksplit > 1, batches of kGemmFoldMinRows rows or more): one
+    // workgroup walks the ksplit ranges of its tile in order, each from zero,
+    // and stores their sum taken in split order ((p0 + p1) + p2) + ... at y --
+    // the value a consumer forms from the partials, so the same bits in one
+    // buffer
+    int fold = 0;
     uint16_t *ot = nullptr;              // SwiGLU output pair, operand-tile layout, K = seg[0].rows
     float *osum = nullptr;               // SwiGLU at M <= 16: per-32 block sums of ot [M][seg[0].rows / 32], or null
     int mode = kGemmStore;
@@ -129,6 +135,13 @@ __host__ __device__ inline int gemm_split_blocks(int nblk, int ksplit)
 {
     return (((nblk + ksplit - 1) / ksplit) + 1) & ~1;
 }
+// Batches from this many rows take the store-mode GEMMs with their K-split
+// partials summed inside the GEMM (GemmArgs::fold): there the partial
+// buffers' HBM round trip through the consumer costs more than the GEMM's
+// own extra accumulator set.  Q5_1 keeps the partials (its large-batch tile
+// has no registers to spare).
+constexpr int kGemmFoldMinRows = 8192;
+inline bool gemm_fold(int type, int M, int ksplit) { return ksplit > 1 && M >= kGemmFoldMinRows && type != kQ5_1; }
 // K-split count of a store-mode GEMM with N outputs and K inputs: up to 4
 // splits of at least 8 blocks, so that narrow projections of small batches
 // still fill the GPU.  A function of the weight shape only.

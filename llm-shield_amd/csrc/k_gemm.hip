@@ -475,11 +475,17 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
 // (whose B tile goes through LDS and whose A fragments come per wave from
 // L2).  The arithmetic per output is the same sequence of MFMAs and FMAs, so
 // the two variants agree bit for bit and either may serve any M.
-template <int TYPE, int MODE, int TM, int TN, int PD, int OCC>
+//
+// FOLD: the workgroup walks every K-split range of its tile in order (the
+// grid has no split dimension), each range's chain from zero as a split
+// workgroup would run it, and keeps the ranges' sum in split order in a
+// second accumulator set; it stores that sum once instead of ksplit partials.
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false>
 __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, int nt, int gm)
 {
     constexpr int BM = 16 * TM, BN = 64 * TN;
     constexpr int U = PD + 1; // weight register ring
+    static_assert(!FOLD || MODE == kGemmStore, "folded K splits are a store-mode form");
     __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * 4 * 512]; // [mi][block][part] operand tiles
 
     // ---- tile of this workgroup (same order and K splits as gemm_q_kernel)
@@ -487,8 +493,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     const int per_xcd = total >> 3;
     const int L = blockIdx.x;
     int Lp = (L & 7) * per_xcd + (L >> 3);
-    const int tiles8 = total / a.ksplit;
-    const int z = Lp / tiles8;
+    const int tiles8 = FOLD ? total : total / a.ksplit;
+    const int z = FOLD ? 0 : Lp / tiles8;
     Lp -= z * tiles8;
     const int group = gm * nt;
     const int first_m = (Lp / group) * gm;
@@ -505,7 +511,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     const int M = a.M, K = a.K, nblk = K >> 5;
     const int nb_per = gemm_split_blocks(nblk, a.ksplit);
     const int kb_begin = z * nb_per;
-    const int nb = min(nblk - kb_begin, nb_per);
+    const int nb = FOLD ? nblk : min(nblk - kb_begin, nb_per); // blocks this workgroup walks
     const int nstage = (nb + 1) >> 1;
     const int m0 = tile_m * BM;
 
@@ -604,6 +610,24 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // FOLD: the finished ranges' sum in split order; a range of spr stages ends
+    // after stage done - 1 when done is a multiple of spr
+    floatx4 tot[FOLD ? TM : 1][FOLD ? TN : 1];
+    const int spr = nb_per >> 1;
+    auto fold_range = [&](int done) __attribute__((always_inline)) {
+        if constexpr (FOLD) {
+            if (done % spr != 0 || done >= nstage) return;
+            const bool first = done == spr;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) tot[i][j][r] = first ? acc[i][j][r] : tot[i][j][r] + acc[i][j][r];
+                    acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+        }
+    };
 
     // Large tiles: the scale FMAs of a tile trail its MFMA pair by two pairs
     // (the result is ready by then, so the vector ALU works beside the matrix
@@ -702,6 +726,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     auto stage = [&](auto jc, int s) __attribute__((always_inline)) {
         constexpr int j = decltype(jc)::value;
         compute(s, s & 1, br[j]);
+        fold_range(s + 1);
         store_a((s + 1) & 1, araw[(j + 1) % UA]);
         load_a(s + 1 + UA, araw[(j + 1) % UA]);
         load_b(s + U, br[j]);
@@ -724,6 +749,17 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
         if constexpr (U > 1) if (rem > 0) stage(std::integral_constant<int, 0>{}, s0);
         if constexpr (U > 2) if (rem > 1) stage(std::integral_constant<int, 1 % U>{}, s0 + 1);
         if constexpr (U > 3) if (rem > 2) stage(std::integral_constant<int, 2 % U>{}, s0 + 2);
+    }
+
+    if constexpr (FOLD) {
+        if (nstage > spr) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = tot[i][j][r] + acc[i][j][r];
+        }
     }
 
     // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
@@ -1040,7 +1076,7 @@ static hipError_t launch_skinny(const GemmArgs &a, hipStream_t s)
 
 // gm_cap: M tiles per group of the tile order (the tiles of a group that share
 // an N column run on one XCD, so its L2 serves their common weight tile).
-template <int TYPE, int MODE, int TM, int TN, int PD, int OCC>
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false>
 static hipError_t launch_bd(const GemmArgs &a, hipStream_t s, int gm_cap = 8)
 {
     constexpr int BM = 16 * TM, BN = 64 * TN;
@@ -1056,9 +1092,9 @@ static hipError_t launch_bd(const GemmArgs &a, hipStream_t s, int gm_cap = 8)
     }
     int gm = mt <= gm_cap ? mt : gm_cap;
     int tiles = mt * ncols;
-    int grid = ((tiles + 7) & ~7) * a.ksplit;
-    launch_stamped(a.ev_start, a.ev_stop, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC>, dim3(grid), dim3(256), 0, s, a, mt,
-                   ncols, gm);
+    int grid = ((tiles + 7) & ~7) * (FOLD ? 1 : a.ksplit);
+    launch_stamped(a.ev_start, a.ev_stop, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC, FOLD>, dim3(grid), dim3(256), 0, s, a,
+                   mt, ncols, gm);
     return hipGetLastError();
 }
 
@@ -1108,7 +1144,11 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
         if (bd_ok) return launch_bd<TYPE, MODE, 2, 2, 1, 4>(a, s);
         return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
     }
-    if (bd_ok) return launch_bd<TYPE, MODE, 4, 4, 1, 2>(a, s);
+    if (bd_ok) {
+        if constexpr (MODE == kGemmStore && TYPE != kQ5_1)
+            if (a.fold) return launch_bd<TYPE, MODE, 4, 4, 1, 2, true>(a, s);
+        return launch_bd<TYPE, MODE, 4, 4, 1, 2>(a, s);
+    }
     return launch_cfg<TYPE, MODE, 4, 1, 2, 8, 1, 1, 2>(a, s);
 }
 
@@ -1133,6 +1173,11 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s)
     if (a.mode == kGemmSwiGlu && (a.nseg != 2 || a.seg[0].rows != a.seg[1].rows || a.seg[0].rows % 32 != 0))
         return hipErrorInvalidValue;
     if (a.osum && (a.mode != kGemmSwiGlu || a.M > 16)) return hipErrorInvalidValue; // written by the skinny kernel only
+    // the folded form exists for the large-batch store tiles (the caller asks
+    // for it exactly when gemm_fold says so)
+    if (a.fold && (a.mode != kGemmStore || !gemm_fold(a.seg[0].type, a.M, a.ksplit))) return hipErrorInvalidValue;
+    for (int i = 0; a.fold && i + 1 < a.nseg; i++)
+        if (a.seg[i].rows % 256 != 0) return hipErrorInvalidValue;
     switch (a.seg[0].type) {
     case kQ8_0: return launch_typed<kQ8_0>(a, s);
     case kQ4_0: return launch_typed<kQ4_0>(a, s);

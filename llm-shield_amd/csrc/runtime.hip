@@ -430,6 +430,7 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
     g.ldy = ldy;
     g.y = y;
     g.ksplit = ksplit;
+    g.fold = gemm_fold(ws[0]->type, T, ksplit) ? 1 : 0; // one buffer: stored_parts() is 1
     g.ev_start = ps.a;
     g.ev_stop = ps.z;
     HIP_TRY(launch_gemm(g, c->stream));
@@ -439,6 +440,11 @@ int linear(jev_ctx *c, int T, const QWeight *const *ws, int nw, const uint16_t *
 // Tokens per decode-attention launch of a single-token-rows pass: the chunk
 // partials of one launch stay within kSingleRowsChunks.
 int single_rows_group(int T, int max_chunks) { return std::max(1, std::min(T, kSingleRowsChunks / std::max(1, max_chunks))); }
+
+// K-split partials a store-mode projection of T tokens leaves for its
+// consumer: its split count, or one buffer when the GEMM sums them itself
+// (gemm_fold); the GEMV path (T == 1) always leaves its partials.
+int stored_parts(int T, const QWeight &w, int ksplit) { return T >= 2 && gemm_fold(w.type, T, ksplit) ? 1 : ksplit; }
 
 int ensure_workspace(jev_ctx *c, int T, int n_out, int mode, int max_chunks, bool single_rows = false)
 {
@@ -788,7 +794,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         na.D = D;
         na.h = c->h.p;
         na.add = l > 0 ? c->ydown.p : nullptr;
-        na.nadd = s_down;
+        na.nadd = l > 0 ? stored_parts(T, c->layers[l - 1].down, s_down) : 1;
         na.add_stride = stride_d;
         na.w = L.attn_norm;
         na.eps = f.rms_eps;
@@ -834,7 +840,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
         ra.k_in = c->y.p + qdim;
         ra.v_in = c->y.p + qdim + kvdim;
         ra.ld_in = ldqkv;
-        ra.nin = s_qkv;
+        ra.nin = stored_parts(T, L.q, s_qkv);
         ra.in_stride = (size_t)T * ldqkv;
         ra.q_out = c->q.p;
         ra.kc = kc;
@@ -974,12 +980,12 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
                             T == 1 ? &dchunks : nullptr);
             if (rc) return rc;
         }
-        CAP_TRY(cap_partials(c, cap, layer_tap(l, "attn_out"), c->yo.p, s_o, T, D));
+        CAP_TRY(cap_partials(c, cap, layer_tap(l, "attn_out"), c->yo.p, stored_parts(T, L.o, s_o), T, D));
 
         // FFN norm (+ attention residual)
         NormArgs nf = na;
         nf.add = c->yo.p;
-        nf.nadd = s_o;
+        nf.nadd = stored_parts(T, L.o, s_o);
         nf.w = L.ffn_norm;
         nf.xsum = (T > 1 && L.gate.type == kQ5_1) ? c->xsum.p : nullptr;
         HIP_TRY(launch_rmsnorm(nf, s));
@@ -1039,7 +1045,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             int rc = linear(c, T, wd, 1, c->ft.p, down_sums, c->f32.p, c->ydown.p, D, s_down, gu_rows ? f.ffn : 0);
             if (rc) return rc;
         }
-        CAP_TRY(cap_partials(c, cap, layer_tap(l, "ffn_out"), c->ydown.p, s_down, T, D));
+        CAP_TRY(cap_partials(c, cap, layer_tap(l, "ffn_out"), c->ydown.p, stored_parts(T, L.down, s_down), T, D));
         if (cap && l == f.n_layers - 1) {
             // the last layer's residual is folded into the final norm of the
             // output rows; h + ffn_out is that same single fp32 add
@@ -1060,7 +1066,7 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     fn.D = D;
     fn.h = c->h.p;
     fn.add = c->ydown.p;
-    fn.nadd = s_down;
+    fn.nadd = stored_parts(T, c->layers[f.n_layers - 1].down, s_down);
     fn.add_stride = stride_d;
     fn.store_h = false;
     fn.w = c->out_norm;
@@ -2089,6 +2095,7 @@ struct MatmulBufs {
 struct MatmulNeeds {
     size_t xt = 0, xsum = 0, part = 0, xq = 0, xd = 0, xs = 0, xqs = 0;
     int ksplit = 1;
+    bool fold = false; // the GEMM sums its K splits itself (gemm_fold): no partials buffer
     bool integer = false;
 };
 static MatmulNeeds matmul_needs(const QWeight &w, int tokens, bool integer)
@@ -2102,7 +2109,8 @@ static MatmulNeeds matmul_needs(const QWeight &w, int tokens, bool integer)
         return n;
     }
     n.ksplit = jev_ctx::split(tokens, w.rows, w.cols);
-    if (n.ksplit > 1) n.part = (size_t)tokens * w.rows * n.ksplit * sizeof(float);
+    n.fold = tokens >= 2 && gemm_fold(w.type, tokens, n.ksplit);
+    if (n.ksplit > 1 && !n.fold) n.part = (size_t)tokens * w.rows * n.ksplit * sizeof(float);
     if (tokens >= 2) {
         n.xt = t16 * w.cols * 2 * sizeof(uint16_t);
         if (w.type == kQ5_1) n.xsum = ((size_t)tokens * nb + 1) * sizeof(float);
@@ -2148,7 +2156,8 @@ static hipError_t matmul_run(const QWeight &w, const float *x, int tokens, float
 {
     if (n.integer) return matmul_integer(w, x, tokens, y, b, s);
     const int rows = w.rows, cols = w.cols;
-    float *dst = n.ksplit > 1 ? b.part : y;
+    const bool partials = n.ksplit > 1 && !n.fold;
+    float *dst = partials ? b.part : y;
     hipError_t e = hipSuccess;
     if (tokens >= 2) {
         e = launch_split(x, tokens, cols, b.xt, s);
@@ -2163,6 +2172,7 @@ static hipError_t matmul_run(const QWeight &w, const float *x, int tokens, float
             g.ldy = rows;
             g.y = dst;
             g.ksplit = n.ksplit;
+            g.fold = n.fold ? 1 : 0;
             e = launch_gemm(g, s);
         }
     } else {
@@ -2174,7 +2184,7 @@ static hipError_t matmul_run(const QWeight &w, const float *x, int tokens, float
         g.ksplit = n.ksplit;
         e = launch_gemv(g, s);
     }
-    if (e == hipSuccess && n.ksplit > 1) e = launch_reduce_partials(dst, n.ksplit, tokens, rows, y, s);
+    if (e == hipSuccess && partials) e = launch_reduce_partials(dst, n.ksplit, tokens, rows, y, s);
     return e;
 }
 

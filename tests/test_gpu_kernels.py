@@ -119,3 +119,25 @@ def test_gpu_resident_weight_matches_test_hook_bitwise(gpu, t, rows, cols, token
     assert np.array_equal(got, matmul_gpu(t, raw, rows, cols, x, tokens))
     if rows * cols * tokens <= 384 * 1088 * 700:
         assert worst_close(oracle.matmul(t, raw, rows, cols, x, tokens), got) <= 1e-4
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+def test_gpu_folded_k_splits_equal_the_summed_partials_bitwise(gpu, t):
+    # From 8192 rows the resident-weight seam's GEMM walks its four K-split
+    # ranges in one workgroup and stores their sum in split order (Q8_0, Q4_0);
+    # the test hook keeps four partial buffers and sums them after.  Same bits,
+    # and each row as it comes out of a small batch.
+    import torch
+    rows, cols, tokens = 3072, 4096, 8200
+    raw = jev.synth_tensor("fold", t, rows, cols, 0.02, seed=9)
+    x = np.random.default_rng(11).standard_normal((tokens, cols)).astype(np.float32)
+    w = jev.QuantWeight(t, rows, cols, raw)
+    dx = torch.from_numpy(x).to("cuda:0")
+    dy = torch.empty((tokens, rows), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    w.matmul_device(dx.data_ptr(), tokens, dy.data_ptr())
+    w.sync()
+    got = dy.cpu().numpy()
+    w.close()
+    assert np.array_equal(got, matmul_gpu(t, raw, rows, cols, x, tokens))
+    assert np.array_equal(got[8000:8017], matmul_gpu(t, raw, rows, cols, x[8000:8017], 17))
