@@ -114,8 +114,9 @@ struct jev_ctx {
     // never outlives the call it was aimed at.
     std::atomic<uint64_t> active{0}, cancel_id{0};
     uint64_t calls = 0;
-    // One event per layer in flight: the host stays at most kLeadLayers layers
-    // ahead of the device so that a cancel stops the work within that many layers.
+    // One event per group of layers (a forward pass) or per step (a greedy
+    // decode) in flight: the host stays at most kLeadLayers groups or steps
+    // ahead of the device, so that a cancel stops the work within that many.
     static constexpr int kLayerEvents = 4, kLeadLayers = 2;
     hipEvent_t layer_ev[kLayerEvents] = {};
 
@@ -142,6 +143,12 @@ struct jev_ctx {
     AttnTile *pin_tiles = nullptr;
     size_t pin_tiles_n = 0;
     hipEvent_t copied = nullptr;
+    // Pinned landing buffer of the outputs a call returns to the host: a
+    // device-to-pageable copy of the 512 KiB logits cost ~80 us more than a
+    // copy to pinned memory plus a host memcpy.  Every call that uses it
+    // drains the stream before returning, so it is free between calls.
+    float *pin_out = nullptr;
+    size_t pin_out_n = 0;
 
     // Kernel timing (jev_profile_enable).
     struct ProfRec {
@@ -749,10 +756,27 @@ std::string layer_tap(int l, const char *tap)
     return b;
 }
 
+// Layers per throttle group of a pass of T tokens: about kThrottleGroupFlops
+// of linear work (~0.5 ms at the GEMMs' large-batch rate) per group, at most
+// half the layers.  Each event marker in the stream costs the device several
+// microseconds (one per layer added 3 % to a 256-token prefill), so short
+// passes record a few per pass; passes of thousands of tokens keep one per
+// layer.
+constexpr double kThrottleGroupFlops = 2.0e11;
+int throttle_group(const jev_ctx *c, int T)
+{
+    const jev_config &f = c->cfg;
+    const double params = (double)f.hidden * (c->qdim() + 2 * c->kvdim()) + (double)c->qdim() * f.hidden +
+                          3.0 * f.ffn * f.hidden;
+    const double k = std::ceil(kThrottleGroupFlops / std::max(2.0 * T * params, 1.0));
+    return (int)std::max(1.0, std::min(k, (double)std::max(1, f.n_layers / 2)));
+}
+
 // `call` (optional) is the cancellable call this pass belongs to: its cancel
-// flag is checked before every layer; with `throttle` the host also waits
-// until the device has finished the layer kLeadLayers back before enqueuing
-// the next, so a cancel stops the pass within that many layers.
+// flag is checked before every layer; with `throttle` the host also waits,
+// before each group of throttle_group layers, until the device has finished
+// the group kLeadLayers back, so a cancel stops the pass within that many
+// groups.
 // With `cap` (a causal call of jev_capture) every tap is recorded as the pass
 // produces it; the one-token pass then runs RoPE before the decode attention
 // instead of inside it, so the rotated queries exist in memory.
@@ -778,9 +802,10 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
     const size_t stride_d = (size_t)T * D; // floats between partials of yo / ydown
     HIP_TRY(launch_gather(c->embd, p.d_tokens, T, c->h.p, s));
     CAP_TRY(cap_add(c, cap, "embeddings", c->h.p, T, D));
+    const int tg = throttle ? throttle_group(c, T) : 1;
     for (int l = 0; l < f.n_layers; l++) {
-        if (call && throttle && l >= jev_ctx::kLeadLayers)
-            HIP_TRY(hipEventSynchronize(c->layer_ev[(l - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]));
+        if (call && throttle && l % tg == 0 && l / tg >= jev_ctx::kLeadLayers)
+            HIP_TRY(hipEventSynchronize(c->layer_ev[(l / tg - jev_ctx::kLeadLayers) % jev_ctx::kLayerEvents]));
         if (call && call->cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled at layer %d", l);
         const Layer &L = c->layers[l];
         float *kc = c->kc + (size_t)l * c->layer_stride();
@@ -1054,7 +1079,8 @@ int enqueue_forward(jev_ctx *c, const Plan &p, int mode, int n_rows, float *dout
             for (size_t i = 0; i < o.v.size(); i++) o.v[i] = hp[i] + o.v[i];
             cap->taps.push_back(std::move(o));
         }
-        if (call && throttle) HIP_TRY(hipEventRecord(c->layer_ev[l % jev_ctx::kLayerEvents], s));
+        if (call && throttle && (l % tg == tg - 1 || l == f.n_layers - 1))
+            HIP_TRY(hipEventRecord(c->layer_ev[(l / tg) % jev_ctx::kLayerEvents], s));
     }
 
     // Heads.  The last layer's FFN residual is folded into the final norm of
@@ -1143,6 +1169,23 @@ int check_ready(jev_ctx *c)
     if (!c) return fail(JEV_EINVAL, "null context");
     if (!c->finalized) return fail(JEV_ESTATE, "jev_finalize has not succeeded on this context");
     HIP_TRY(hipSetDevice(c->device));
+    return JEV_OK;
+}
+
+// Copies n floats of device output to the caller's host buffer through the
+// pinned landing buffer, draining the stream (the call's synchronisation).
+int copy_out(jev_ctx *c, float *host, const float *dev, size_t n)
+{
+    if (n > c->pin_out_n) {
+        if (c->pin_out) HIP_TRY(hipHostFree(c->pin_out));
+        c->pin_out = nullptr;
+        c->pin_out_n = 0;
+        HIP_TRY(hipHostMalloc((void **)&c->pin_out, n * sizeof(float), hipHostMallocDefault));
+        c->pin_out_n = n;
+    }
+    if (n) HIP_TRY(hipMemcpyAsync(c->pin_out, dev, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (n) std::memcpy(host, c->pin_out, n * sizeof(float));
     return JEV_OK;
 }
 
@@ -1265,6 +1308,7 @@ void jev_destroy(jev_ctx *c)
     c->part.release(); c->xsum.release(); c->cap32.release(); c->xt.release(); c->ft.release(); c->ints.release(); c->dec_state.release(); c->tiles.release(); c->amax_v.release(); c->amax_i.release();
     if (c->pin_ints) (void)hipHostFree(c->pin_ints);
     if (c->pin_tiles) (void)hipHostFree(c->pin_tiles);
+    if (c->pin_out) (void)hipHostFree(c->pin_out);
     if (c->copied) (void)hipEventDestroy(c->copied);
     for (auto e : c->layer_ev)
         if (e) (void)hipEventDestroy(e);
@@ -1560,8 +1604,8 @@ int jev_forward(jev_ctx *c, const int32_t *tokens, int32_t T, const jev_layout *
         (void)hipStreamSynchronize(c->stream);
         return rc;
     }
-    if (need) HIP_TRY(hipMemcpyAsync(out, dout, need * sizeof(float), hipMemcpyDeviceToHost, c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    rc = copy_out(c, out, dout, need);
+    if (rc) return rc;
     // a cancel that landed after the last layer was enqueued still cancels
     // this call: the cache length stays where it was (KvCache.Advance is skipped)
     if (call.cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled");
@@ -1589,9 +1633,8 @@ int jev_capture(jev_ctx *c, const int32_t *tokens, int32_t T, jev_sink sink, voi
         (void)hipStreamSynchronize(c->stream);
         return rc;
     }
-    HIP_TRY(hipMemcpyAsync(logits, c->logits.p, (size_t)c->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost,
-                           c->stream));
-    HIP_TRY(hipStreamSynchronize(c->stream));
+    rc = copy_out(c, logits, c->logits.p, (size_t)c->cfg.vocab);
+    if (rc) return rc;
     if (call.cancelled()) return fail(JEV_ECANCELED, "the forward pass was cancelled");
     c->len = std::max(c->len, p.end); // KvCache.Advance (MinistralModel.cs:360)
     for (const Capture::Tap &t : cap.taps) sink(user, t.name.c_str(), t.v.data(), t.rows, t.cols);
