@@ -209,10 +209,12 @@ int jev_margins(const float *verdicts, int32_t n_options, int32_t n_yes, int32_t
  * cancels the call in flight on ctx -- jev_forward, jev_forward_tree,
  * jev_decode_greedy, jev_capture -- which then returns JEV_ECANCELED with the
  * cache length unchanged (greedy decoding: advanced by the steps that ran).
- * Those calls keep at most two layers (decode: two steps) enqueued ahead of
- * the device and check between them, so the work stops within that many
- * layers; a cancel that lands after the last layer was enqueued still cancels
- * the call.  A cancel aimed at no call (none in flight) does nothing, so it
+ * Those calls keep at most two groups of layers (decode: two steps) enqueued
+ * ahead of the device and check between layers, so the work stops within that
+ * many; a group is about 2e11 FLOPs of linear work (one layer from a few
+ * thousand tokens, a few layers at a few hundred, half the model for one
+ * token).  A cancel that lands after the last layer was enqueued still
+ * cancels the call.  A cancel aimed at no call (none in flight) does nothing, so it
  * never reaches a later call.  The only entry point safe from another thread. */
 void jev_cancel(jev_ctx *ctx);
 
