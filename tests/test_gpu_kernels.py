@@ -122,14 +122,16 @@ def test_gpu_resident_weight_matches_test_hook_bitwise(gpu, t, rows, cols, token
 
 
 @pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
-def test_gpu_folded_k_splits_equal_the_summed_partials_bitwise(gpu, t):
+@pytest.mark.parametrize("cols", [4096, 4128])
+def test_gpu_folded_k_splits_equal_the_summed_partials_bitwise(gpu, t, cols):
     # From 8192 rows the resident-weight seam's GEMM walks its four K-split
     # ranges in one workgroup and stores their sum in split order (Q8_0, Q4_0);
     # the test hook keeps four partial buffers and sums them after.  Same bits,
-    # and each row as it comes out of a small batch.
+    # and each row as it comes out of a small batch.  4128 columns: 129 quant
+    # blocks, a short last range ending in a half stage.
     import torch
-    rows, cols, tokens = 3072, 4096, 8200
-    raw = jev.synth_tensor("fold", t, rows, cols, 0.02, seed=9)
+    rows, tokens = 3072, 8200
+    raw = jev.synth_tensor(f"fold{cols}", t, rows, cols, 0.02, seed=9)
     x = np.random.default_rng(11).standard_normal((tokens, cols)).astype(np.float32)
     w = jev.QuantWeight(t, rows, cols, raw)
     dx = torch.from_numpy(x).to("cuda:0")
