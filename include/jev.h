@@ -259,7 +259,9 @@ int jev_weight_create(int ggml_type, int64_t rows, int64_t cols, const void *byt
 void jev_weight_destroy(jev_weight *w);
 /* y = x . W^T with x [tokens][cols] and y [tokens][rows], both fp32 device
  * pointers; tokens >= 2 take the MFMA GEMM, 1 token the GEMV (the dispatch of
- * QuantMatMul.cs:84-101).  Only enqueues on the weight's stream. */
+ * QuantMatMul.cs:84-101).  Only enqueues on the weight's stream.  Any float
+ * alignment; at 16 bytes the fp16-pair split of x and the K-split sum into y
+ * move 16 bytes per access (the result bits are the same). */
 int jev_matmul_device(jev_weight *w, const float *x, int32_t tokens, float *y);
 /* jev_matmul_device without any allocation.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory during the call (code

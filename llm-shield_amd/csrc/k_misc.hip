@@ -568,12 +568,48 @@ __global__ void split_kernel(const float *x, int T, int D, uint16_t *xt)
     xt[xt_index(t, k, D >> 5, 1)] = b;
 }
 
+// The same split in the tiles' lane order: one wave per (16-row group, quant
+// block) tile, lane l taking row l % 16 and k = 8 (l / 16) .. + 7 -- two
+// 16-byte loads, and one contiguous 1 KiB store per part for the wave.  Rows
+// past T (the tile's padding) are written as zeros.  x 16-byte aligned.
+__global__ __launch_bounds__(256) void split_tile_kernel(const float *x, int T, int D, uint16_t *xt)
+{
+    const int nblk = D >> 5, lane = threadIdx.x & 63;
+    const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (tile >= ((T + 15) >> 4) * nblk) return;
+    const int t = (tile / nblk) * 16 + (lane & 15), k = (tile % nblk) * 32 + 8 * (lane >> 4);
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (t < T) {
+        const float4 *xp = (const float4 *)(x + (size_t)t * D + k);
+        v0 = xp[0];
+        v1 = xp[1];
+    }
+    const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        uint16_t h0, l0, h1, l1;
+        split_f16(v[j], h0, l0);
+        split_f16(v[j + 1], h1, l1);
+        hw[j >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        lw[j >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+    uint16_t *o = xt + (size_t)tile * 1024 + 8 * lane; // xt_index(t, k, nblk, 0)
+    *(uint4 *)o = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(o + 512) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
 hipError_t launch_split(const float *x, int T, int D, uint16_t *xt, hipStream_t s)
 {
     size_t n = (size_t)T * D;
     if (n == 0) return hipSuccess;
     if (D % 32 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, T, D, xt);
+    if ((uintptr_t)x % 16 == 0) {
+        const size_t tiles = (size_t)((T + 15) / 16) * (D / 32);
+        hipLaunchKernelGGL(split_tile_kernel, dim3((unsigned)((tiles + 3) / 4)), dim3(256), 0, s, x, T, D, xt);
+    } else {
+        hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, T, D, xt);
+    }
     return hipGetLastError();
 }
 
@@ -588,10 +624,38 @@ __global__ void reduce_partials_kernel(const float *p, int ksplit, size_t mn, fl
     y[i] = s;
 }
 
+// Four outputs per thread, the partials added in the same order (mn % 4 == 0,
+// p and y 16-byte aligned); every partial's load issued before the first add.
+template <int KS>
+__global__ __launch_bounds__(256) void reduce_partials4_kernel(const float *p, size_t mn, float *y)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * i >= mn) return;
+    float4 v[KS];
+#pragma unroll
+    for (int z = 0; z < KS; z++) v[z] = ((const float4 *)(p + (size_t)z * mn))[i];
+    float4 s = v[0];
+#pragma unroll
+    for (int z = 1; z < KS; z++) {
+        s.x = s.x + v[z].x;
+        s.y = s.y + v[z].y;
+        s.z = s.z + v[z].z;
+        s.w = s.w + v[z].w;
+    }
+    ((float4 *)y)[i] = s;
+}
+
 hipError_t launch_reduce_partials(const float *partial, int ksplit, int M, int N, float *y, hipStream_t s)
 {
     size_t mn = (size_t)M * N;
     if (mn == 0) return hipSuccess;
+    if (mn % 4 == 0 && (uintptr_t)partial % 16 == 0 && (uintptr_t)y % 16 == 0 && ksplit >= 2 && ksplit <= 4) {
+        const dim3 grid((unsigned)((mn / 4 + 255) / 256));
+        if (ksplit == 2) hipLaunchKernelGGL(reduce_partials4_kernel<2>, grid, dim3(256), 0, s, partial, mn, y);
+        else if (ksplit == 3) hipLaunchKernelGGL(reduce_partials4_kernel<3>, grid, dim3(256), 0, s, partial, mn, y);
+        else hipLaunchKernelGGL(reduce_partials4_kernel<4>, grid, dim3(256), 0, s, partial, mn, y);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, partial, ksplit, mn, y);
     return hipGetLastError();
 }

@@ -122,6 +122,31 @@ def test_gpu_resident_weight_matches_test_hook_bitwise(gpu, t, rows, cols, token
 
 
 @pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
+def test_gpu_resident_weight_unaligned_buffers_give_the_same_bits(gpu, t):
+    # x and y one float past a 16-byte boundary take the one-element split and
+    # partial-sum kernels instead of the vector ones: the same arithmetic
+    import torch
+    rows, cols, tokens = 384, 1088, 130
+    raw = jev.synth_tensor(f"una{rows}x{cols}", t, rows, cols, 0.02, seed=3)
+    x = np.random.default_rng(5).standard_normal((tokens, cols)).astype(np.float32)
+    w = jev.QuantWeight(t, rows, cols, raw)
+    bx = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)])).to("cuda:0")
+    by = torch.zeros(tokens * rows + 1, dtype=torch.float32, device="cuda:0")
+    dx = torch.from_numpy(x).to("cuda:0")
+    dy = torch.empty((tokens, rows), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    assert bx.data_ptr() % 16 == 0 and by.data_ptr() % 16 == 0
+    w.matmul_device(bx.data_ptr() + 4, tokens, by.data_ptr() + 4)
+    w.matmul_device(dx.data_ptr(), tokens, dy.data_ptr())
+    w.sync()
+    got = by.cpu().numpy()
+    want = dy.cpu().numpy()
+    w.close()
+    assert got[0] == 0.0
+    assert np.array_equal(got[1:].reshape(tokens, rows), want)
+
+
+@pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
 @pytest.mark.parametrize("cols", [4096, 4128])
 def test_gpu_folded_k_splits_equal_the_summed_partials_bitwise(gpu, t, cols):
     # From 8192 rows the resident-weight seam's GEMM walks its four K-split
