@@ -480,12 +480,20 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
 // grid has no split dimension), each range's chain from zero as a split
 // workgroup would run it, and keeps the ranges' sum in split order in a
 // second accumulator set; it stores that sum once instead of ksplit partials.
-template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false>
-__global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, int nt, int gm)
+//
+// NW: waves per workgroup, side by side along N (BN = 16 TN NW).  Twelve
+// waves share one activation tile three times as wide as four do: a third of
+// the activation loads and LDS stores per MFMA.  At 256 rows of the 3B
+// projections that gives 256 workgroups of 12 waves, one per CU and the same
+// three waves per SIMD as 768 workgroups of four (QKV 27.4 -> 26.2 us, O 20.0
+// -> 19.2, down 39.1 -> 36.2; cold weights).
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int mt, int nt, int gm)
 {
-    constexpr int BM = 16 * TM, BN = 64 * TN;
+    constexpr int BM = 16 * TM, BN = 16 * TN * NW;
     constexpr int U = PD + 1; // weight register ring
     static_assert(!FOLD || MODE == kGemmStore, "folded K splits are a store-mode form");
+    static_assert(NW % 4 == 0, "whole groups of four waves");
     __shared__ __attribute__((aligned(16))) uint16_t As[2][TM * 4 * 512]; // [mi][block][part] operand tiles
 
     // ---- tile of this workgroup (same order and K splits as gemm_q_kernel)
@@ -515,21 +523,32 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     const int nstage = (nb + 1) >> 1;
     const int m0 = tile_m * BM;
 
-    // ---- activation loader: thread -> fragment f = tid / 64 (block f >> 1,
-    // part f & 1) of every row group mi, lane slot tid % 64: 16 bytes each.
+    // ---- activation loader: the stage's TM * 4 fragments (row group mi,
+    // block f >> 1, part f & 1 for fragment 4 mi + f) of 1 KiB go to the waves
+    // round robin, wave w taking fragments w, w + NW, ...; each lane loads its
+    // 16-byte slot.  With four waves, wave w takes fragment f = w of every row
+    // group.  Past the last fragment a wave repeats it (the same bytes to the
+    // same LDS slot).
     const int rg_last = (M - 1) >> 4; // groups past M feed unstored rows
     const rsrc_t ra = make_rsrc(a.xt, (uint32_t)(rg_last + 1) * nblk * 2048);
-    const int af = wave, abb = af >> 1, apart = af & 1;
-    uint32_t va[TM];
+    constexpr int NCH = TM * 4, AL = (NCH + NW - 1) / NW;
+    int ach[AL], abb[AL];
+    uint32_t va[AL];
 #pragma unroll
-    for (int mi = 0; mi < TM; mi++)
-        va[mi] = (((uint32_t)min((m0 >> 4) + mi, rg_last) * nblk * 2 + apart) * 512 + lane * 8) * 2;
+    for (int j = 0; j < AL; j++) {
+        // four waves: fragment `wave` of row group j (block and part are the wave's for every j)
+        const int ch = NW == 4 ? 4 * j + wave : min(wave + NW * j, NCH - 1);
+        const int mi = NW == 4 ? j : ch >> 2, part = NW == 4 ? wave & 1 : ch & 1;
+        ach[j] = ch;
+        abb[j] = NW == 4 ? wave >> 1 : (ch >> 1) & 1;
+        va[j] = (((uint32_t)min((m0 >> 4) + mi, rg_last) * nblk * 2 + part) * 512 + lane * 8) * 2;
+    }
     // Q5_1 block sums of the stage's BM rows x 2 blocks, one per thread of the
     // first 2 * BM, staged through LDS with the activations.  The block index
     // rides in the per-thread offset so the scalar offset stays uniform; the
     // other threads read past the buffer (zeros).  A missing odd last block
     // reads a finite neighbour that its zero min cancels.
-    __shared__ __attribute__((aligned(16))) float Xs[2][TYPE == kQ5_1 ? 256 : 4]; // [bb * BM + row], the rest unused
+    __shared__ __attribute__((aligned(16))) float Xs[2][TYPE == kQ5_1 ? 64 * NW : 4]; // [bb * BM + row], the rest unused
     rsrc_t rs;
     uint32_t vx = 0;
     if (TYPE == kQ5_1) {
@@ -537,20 +556,21 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
         vx = tid < 2 * BM ? ((uint32_t)(m0 + tid % BM) * nblk + tid / BM) * 4 : 0x40000000u;
     }
     struct AStage {
-        uint4 v[TM];
+        uint4 v[AL];
         float xs;
     };
     auto load_a = [&](int st, AStage &r) __attribute__((always_inline)) {
         st = min(st, nstage - 1);
-        const int kblk = kb_begin + min(2 * st + abb, nb - 1);
 #pragma unroll
-        for (int mi = 0; mi < TM; mi++)
-            r.v[mi] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[mi], kblk * 2048, 0));
+        for (int j = 0; j < AL; j++) {
+            const int kblk = kb_begin + min(2 * st + (NW == 4 ? abb[0] : abb[j]), nb - 1);
+            r.v[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[j], kblk * 2048, 0));
+        }
         if (TYPE == kQ5_1) r.xs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vx, (kb_begin + 2 * st) * 4, 0));
     };
     auto store_a = [&](int buf, const AStage &r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int mi = 0; mi < TM; mi++) *(uint4 *)&As[buf][(mi * 4 + af) * 512 + lane * 8] = r.v[mi];
+        for (int j = 0; j < AL; j++) *(uint4 *)&As[buf][(NW == 4 ? j * 4 + wave : ach[j]) * 512 + lane * 8] = r.v[j];
         if (TYPE == kQ5_1) Xs[buf][tid] = r.xs;
     };
 
@@ -566,13 +586,16 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
             seg = t & 1; // 16-row groups alternate gate and up
             rgw = tile_n * (BN / 32) + (t >> 1);
         } else {
-            int s0 = 0, start = 0, n0 = tile_n * BN;
-            while (s0 + 1 < a.nseg && n0 >= start + a.seg[s0].rows) {
+            // the segment of the workgroup's tile (four waves: a tile never
+            // straddles two) or of this wave's 16 TN rows (which never do)
+            int s0 = 0, start = 0;
+            const int r0 = tile_n * BN + (NW == 4 ? 0 : 16 * t);
+            while (s0 + 1 < a.nseg && r0 >= start + a.seg[s0].rows) {
                 start += a.seg[s0].rows;
                 s0++;
             }
             seg = s0;
-            rgw = (n0 - start) / 16 + t;
+            rgw = (r0 - start) / 16 + (NW == 4 ? t : 0);
         }
         seg = __builtin_amdgcn_readfirstlane(seg);
         const QWeight &w = a.seg[seg];
@@ -765,24 +788,31 @@ __global__ __launch_bounds__(256, OCC) void gemm_bd_kernel(GemmArgs a, int mt, i
     // ---- epilogue.  Lane holds C[4*(lane/16) + r][lane % 16] of each 16x16 tile.
     const int row_base = m0 + 4 * (lane >> 4);
     if (MODE == kGemmStore) {
+        // columns are the segments' rows concatenated; only the last segment
+        // may end inside a tile
         float *y = a.y + (size_t)z * M * a.ldy;
-        int seg = 0, start = 0;
         const int n0 = tile_n * BN;
-        while (seg + 1 < a.nseg && n0 >= start + a.seg[seg].rows) {
-            start += a.seg[seg].rows;
-            seg++;
+        int seg = 0, start = 0, end = 0;
+        if constexpr (NW == 4) {
+            // a four-wave tile lies in one segment
+            while (seg + 1 < a.nseg && n0 >= start + a.seg[seg].rows) {
+                start += a.seg[seg].rows;
+                seg++;
+            }
+            end = start + a.seg[seg].rows;
+        } else {
+            for (int i = 0; i < a.nseg; i++) end += a.seg[i].rows;
         }
-        const QWeight &ws = a.seg[seg];
 #pragma unroll
         for (int n = 0; n < TN; n++) {
-            const int off = (wave * TN + n) * 16 + (lane & 15);
-            if (n0 - start + off >= ws.rows) continue;
+            const int col = n0 + (wave * TN + n) * 16 + (lane & 15);
+            if (col >= end) continue;
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = row_base + 16 * i + r;
-                    if (row < M) y[(size_t)row * a.ldy + n0 + off] = acc[i][n][r];
+                    if (row < M) y[(size_t)row * a.ldy + col] = acc[i][n][r];
                 }
         }
     } else {
@@ -1076,10 +1106,10 @@ static hipError_t launch_skinny(const GemmArgs &a, hipStream_t s)
 
 // gm_cap: M tiles per group of the tile order (the tiles of a group that share
 // an N column run on one XCD, so its L2 serves their common weight tile).
-template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false>
+template <int TYPE, int MODE, int TM, int TN, int PD, int OCC, bool FOLD = false, int NW = 4>
 static hipError_t launch_bd(const GemmArgs &a, hipStream_t s, int gm_cap = 8)
 {
-    constexpr int BM = 16 * TM, BN = 64 * TN;
+    constexpr int BM = 16 * TM, BN = 16 * TN * NW;
     static_assert(MODE != kGemmSwiGlu || TN % 2 == 0, "SwiGLU pairs tiles within a wave");
     int mt = (a.M + BM - 1) / BM;
     int ncols;
@@ -1093,8 +1123,8 @@ static hipError_t launch_bd(const GemmArgs &a, hipStream_t s, int gm_cap = 8)
     int gm = mt <= gm_cap ? mt : gm_cap;
     int tiles = mt * ncols;
     int grid = ((tiles + 7) & ~7) * (FOLD ? 1 : a.ksplit);
-    launch_stamped(a.ev_start, a.ev_stop, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC, FOLD>, dim3(grid), dim3(256), 0, s, a,
-                   mt, ncols, gm);
+    launch_stamped(a.ev_start, a.ev_stop, gemm_bd_kernel<TYPE, MODE, TM, TN, PD, OCC, FOLD, NW>, dim3(grid), dim3(64 * NW), 0, s,
+                   a, mt, ncols, gm);
     return hipGetLastError();
 }
 
@@ -1141,6 +1171,11 @@ static hipError_t launch_mode(const GemmArgs &a, hipStream_t s)
         // in the tile order: 8 % faster than 8 at 256 tokens (the store
         // shapes are indifferent)
         if (MODE == kGemmSwiGlu) return launch_bd<TYPE, MODE, 2, 2, 1, 5>(a, s, 4);
+        // 225..256 rows: 12-wave workgroups (one per CU at the 3B projection
+        // shapes, three waves per SIMD), 4-8 % ahead of 4-wave ones.  Fewer
+        // rows would leave CUs idle, more would need a second round.
+        if constexpr (MODE == kGemmStore)
+            if (bd_ok && a.M > 224 && a.M <= 256) return launch_bd<TYPE, MODE, 2, 2, 1, 1, false, 12>(a, s);
         if (bd_ok) return launch_bd<TYPE, MODE, 2, 2, 1, 4>(a, s);
         return launch_cfg<TYPE, MODE, 4, 1, 1, 4, 2, 2, 2>(a, s);
     }

@@ -86,6 +86,9 @@ def test_gpu_matmul_batch_invariance_bitwise(gpu, t):
     part = matmul_gpu(t, raw, rows, cols, x[120:137], 17)
     assert np.array_equal(full[:300], mid)
     assert np.array_equal(full[120:137], part)
+    # 225..256 rows take the 12-wave workgroups
+    for lo, n in ((0, 256), (300, 240)):
+        assert np.array_equal(full[lo:lo + n], matmul_gpu(t, raw, rows, cols, x[lo:lo + n], n)), n
     # 2..16 tokens take the one-wave-per-row-group kernel: the same chain per output
     for lo, n in ((0, 2), (33, 9), (684, 16)):
         assert np.array_equal(full[lo:lo + n], matmul_gpu(t, raw, rows, cols, x[lo:lo + n], n)), n
