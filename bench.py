@@ -676,8 +676,10 @@ def main():
         result["tree_breakdown_ms"] = {
             "gemm": round(tg[1] / args.tree_steps, 3),
             "gemm_tflops": round(tg[2] / (tg[1] * 1e-3) / 1e12, 2) if tg[1] else None,
+            "gemm_mfma_frac": round(tg[2] / (tg[1] * 1e-3) / PEAK_FP16_MFMA, 4) if tg[1] else None,
             "attention": round(ta[1] / args.tree_steps, 3),
             "attention_tflops": round(ta[2] / (ta[1] * 1e-3) / 1e12, 2) if ta[1] else None,
+            "attention_mfma_frac": round(ta[2] / (ta[1] * 1e-3) / PEAK_FP16_MFMA, 4) if ta[1] else None,
         }
         result["tree_z"] = [round(float(x), 5) for x in z]
         result["boundary"]["tree_jev_forward_tree_ms"] = round(tree_host_ms, 3)
