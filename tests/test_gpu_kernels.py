@@ -59,7 +59,8 @@ def test_gpu_dequant_random_blocks_bit_exact(gpu, t):
 
 
 SHAPES = [(128, 256, 1), (64, 3072, 5), (128, 3072, 13), (64, 4096, 6), (64, 9216, 7), (256, 512, 2),
-          (384, 1024, 130), (3072, 3072, 256), (1024, 3072, 1), (384, 1088, 700), (200, 512, 513)]
+          (384, 1024, 130), (3072, 3072, 256), (1024, 3072, 1), (384, 1088, 700), (200, 512, 513),
+          (200, 1088, 250)]  # the last: 12-wave workgroups over a ragged N
 
 
 @pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
