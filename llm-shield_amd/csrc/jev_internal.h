@@ -34,6 +34,12 @@ int64_t row_bytes(int type, int64_t cols);
 //                          lane's scales and mins are one 8-byte load
 //                          (QWeight::m points at the first min)
 //   qh  (Q5_1)      128 B: lane l's fifth bits at 2 l + block, bit i = element 8 g + i
+//   qb  (Q5_1)     1024 B: the same quants again as whole bytes q in [0, 31], in
+//                          Q8_0's order (lane l's 16 bytes at 16 l), for the
+//                          kernels of two or more tokens: one byte permute and
+//                          one packed subtraction per two weights instead of the
+//                          nibble and fifth-bit assembly (the one-token GEMV keeps
+//                          the 5-bit fields, whose bytes it streams)
 constexpr int kTileRows = 16, kTileK = 64;
 struct QWeight {
     int type = -1;
@@ -42,6 +48,7 @@ struct QWeight {
     const uint16_t *d = nullptr;
     const uint16_t *m = nullptr;
     const uint8_t *qh = nullptr;
+    const uint8_t *qb = nullptr; // Q5_1 quants as bytes (see qb above)
     void *base = nullptr; // owning allocation
     size_t bytes = 0;
 };
@@ -54,7 +61,7 @@ __host__ __device__ inline int tile_d_bytes(int type) { return type == kQ5_1 ? 1
 
 // Byte offsets of the fields inside one allocation of the layout above.
 struct QLayout {
-    size_t qs, d, m, qh, total;
+    size_t qs, d, m, qh, qb, total;
 };
 QLayout qlayout(int type, int64_t rows, int64_t cols);
 

@@ -58,9 +58,9 @@ struct alignas(16) u32x4 {
 // One loader chunk: a lane slot of a weight tile -- the quants of one row
 // at k = 8g .. 8g + 7 of both blocks of the stage -- and that row's scales.
 struct BChunk {
-    uint4 q;       // Q8_0: 16 bytes; Q4_0 / Q5_1: 8 bytes in .x, .y
+    uint4 q;       // bytes (Q8_0, Q5_1's byte copy): 16; nibbles (Q4_0, Q5_1's fields): 8 in .x, .y
     uint32_t d, m; // two fp16 each (block 0 low half)
-    uint32_t qh;   // Q5_1: two bytes (block 0 low byte)
+    uint32_t qh;   // Q5_1 from its 5-bit fields: the lane's fifth bits (block 0 low byte)
 };
 
 // Segment and local row of tile column rr (epilogue).
@@ -88,60 +88,65 @@ __device__ __forceinline__ void map_row(const GemmArgs &a, int tile_n, int rr, i
 // loop free of divergent loads lets the compiler count outstanding loads
 // exactly instead of draining the queue every stage.
 
+// Quants as these kernels read them.  BQ (byte quants): whole bytes, 1 KiB
+// per tile -- Q8_0's (QWeight::qs, stored biased as q + 128) or Q5_1's byte
+// copy (QWeight::qb, q itself).  Otherwise 512 B of nibbles per tile (QWeight::qs:
+// Q4_0, or Q5_1's low four bits with the fifth bits in QWeight::qh).  Q8_0
+// is always bytes, Q4_0 always nibbles; Q5_1 is bytes wherever the kernel's
+// registers allow the 16-byte chunk (all but the 64 x 256 tile): one byte
+// permute and one packed subtraction per two weights instead of the nibble
+// and fifth-bit assembly.  The decoded integers are the same either way.
+template <int TYPE, bool BQ>
+__device__ __forceinline__ rsrc_t quant_rsrc(const QWeight &w, uint32_t tiles)
+{
+    return make_rsrc(TYPE == kQ5_1 && BQ ? w.qb : w.qs, tiles * (BQ ? 1024u : 512u));
+}
+
+// Four quants of a block as two fp16 pairs of exact integers: a byte b placed
+// under the exponent byte is 1024 + b; the bias subtracts 1024 and, for Q8_0's
+// biased bytes or Q4_0's offset 8, that too.
+template <int TYPE, bool BQ>
+__device__ __forceinline__ void decode4(const BChunk &c, int bb, int half, uint32_t &pa, uint32_t &pb)
+{
+    if (BQ) {
+        const uint32_t w = bb ? (half ? c.q.w : c.q.z) : (half ? c.q.y : c.q.x);
+        bytes_to_f16(w, TYPE == kQ8_0 ? (_Float16)1152.0f : (_Float16)1024.0f, pa, pb);
+    } else {
+        // byte i = element i (low nibble) | element i + 4 (high nibble)
+        const uint32_t w = bb ? c.q.y : c.q.x;
+        uint32_t n = half ? (w >> 4) & 0x0f0f0f0fu : w & 0x0f0f0f0fu;
+        _Float16 bias = (_Float16)1032.0f;
+        if (TYPE == kQ5_1) {
+            // fifth bits: spread 4 bits to bit 4 of each byte
+            const uint32_t hb = (c.qh >> (8 * bb)) & 0xffu;
+            n |= ((((half ? hb >> 4 : hb & 15u)) * 0x00204081u) & 0x01010101u) << 4;
+            bias = (_Float16)1024.0f;
+        }
+        bytes_to_f16(n, bias, pa, pb);
+    }
+}
+
 // B fragment of block bb of a loaded chunk: 8 fp16 integers for the lane's
 // row at k = 8g .. 8g + 7.
-template <int TYPE>
+template <int TYPE, bool BQ>
 __device__ __forceinline__ half8_t decode_b_frag(const BChunk &c, int bb)
 {
     uint32_t o0, o1, o2, o3;
-    if (TYPE == kQ8_0) {
-        const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
-        bytes_to_f16(w0, (_Float16)1152.0f, o0, o1);
-        bytes_to_f16(w1, (_Float16)1152.0f, o2, o3);
-    } else {
-        const uint32_t w = bb ? c.q.y : c.q.x;
-        uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
-        _Float16 bias = (_Float16)1032.0f;
-        if (TYPE == kQ5_1) {
-            const uint32_t hb = (c.qh >> (8 * bb)) & 0xffu;
-            n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
-            n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
-            bias = (_Float16)1024.0f;
-        }
-        bytes_to_f16(n0, bias, o0, o1);
-        bytes_to_f16(n1, bias, o2, o3);
-    }
+    decode4<TYPE, BQ>(c, bb, 0, o0, o1);
+    decode4<TYPE, BQ>(c, bb, 1, o2, o3);
     return __builtin_bit_cast(half8_t, make_uint4(o0, o1, o2, o3));
 }
 
 // Decoded quants of one chunk as fp16 integers: block 0 to dst[0..8),
 // block 1 to dst[32..40) (the LDS row of the chunk's weight row).
-template <int TYPE>
+template <int TYPE, bool BQ>
 __device__ __forceinline__ void store_chunk(const BChunk &c, uint16_t *dst)
 {
 #pragma unroll
     for (int bb = 0; bb < 2; bb++) {
         uint32_t o0, o1, o2, o3;
-        if (TYPE == kQ8_0) {
-            // stored biased (q + 128): 1024 + byte under the exponent, minus 1152.
-            const uint32_t w0 = bb ? c.q.z : c.q.x, w1 = bb ? c.q.w : c.q.y;
-            bytes_to_f16(w0, (_Float16)1152.0f, o0, o1);
-            bytes_to_f16(w1, (_Float16)1152.0f, o2, o3);
-        } else {
-            // byte i = element i (low nibble) | element i + 4 (high nibble)
-            const uint32_t w = bb ? c.q.y : c.q.x;
-            uint32_t n0 = w & 0x0f0f0f0fu, n1 = (w >> 4) & 0x0f0f0f0fu;
-            _Float16 bias = (_Float16)1032.0f;
-            if (TYPE == kQ5_1) {
-                // fifth bits: spread 4 bits to bit 4 of each byte
-                const uint32_t hb = (c.qh >> (8 * bb)) & 0xffu;
-                n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
-                n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
-                bias = (_Float16)1024.0f;
-            }
-            bytes_to_f16(n0, bias, o0, o1);
-            bytes_to_f16(n1, bias, o2, o3);
-        }
+        decode4<TYPE, BQ>(c, bb, 0, o0, o1);
+        decode4<TYPE, BQ>(c, bb, 1, o2, o3);
         *(u32x4 *)(dst + 32 * bb) = u32x4{o0, o1, o2, o3};
     }
 }
@@ -204,11 +209,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     // so its weight (segment) is uniform.  Every load is a buffer load: a
     // scalar resource, a per-lane offset fixed for the loop and a scalar
     // per-stage offset; no per-stage vector address arithmetic.
-    rsrc_t rq[CPT], rd[CPT], rh[CPT];
+    rsrc_t rq[CPT], rd[CPT];
     int btile0[CPT]; // first tile of the chunk's row group (uniform)
     int b_lds[CPT], b_ds[CPT];
     const int slot = tid & 63, sg = slot >> 4, sr = slot & 15;
-    const uint32_t vq = (uint32_t)slot * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * sr, vh = 2 * slot;
+    constexpr bool BQ = TYPE != kQ4_0; // byte quants (see quant_rsrc)
+    const uint32_t vq = (uint32_t)slot * (BQ ? 16 : 8), vd = 4 * sr;
     const int kp_begin = kb_begin >> 1; // kb_begin is even
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
@@ -232,9 +238,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
         const QWeight &w = a.seg[seg];
         const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
-        rq[j] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
+        rq[j] = quant_rsrc<TYPE, BQ>(w, tiles);
         rd[j] = make_rsrc(w.d, tiles * tile_d_bytes(TYPE));
-        if (TYPE == kQ5_1) rh[j] = make_rsrc(w.qh, tiles * 128);
         // row groups past the weight feed unstored columns
         btile0[j] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + kp_begin);
         b_lds[j] = own ? (16 * t + sr) * LROW + 8 * sg : BN * LROW;
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
             const int tile = btile0[j] + st;
-            if (TYPE == kQ8_0) {
+            if (BQ) {
                 br[j].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[j], vq, tile * 1024, 0));
             } else {
                 uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[j], vq, tile * 512, 0));
@@ -261,7 +266,6 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
                 const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[j], 2 * vd, tile * 128, 0));
                 br[j].d = dm.x;
                 br[j].m = dm.y;
-                br[j].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[j], vh, tile * 128, 0);
             } else {
                 br[j].d = __builtin_amdgcn_raw_buffer_load_b32(rd[j], vd, tile * 64, 0);
             }
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_q_kernel(GemmArgs a, int mt, in
     auto store_b = [&](int buf, const BChunk (&br)[CPT]) {
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
-            store_chunk<TYPE>(br[j], &Bs[buf][b_lds[j]]);
+            store_chunk<TYPE, BQ>(br[j], &Bs[buf][b_lds[j]]);
             Ds[buf][b_ds[j]] = h2f((uint16_t)br[j].d);
             Ds[buf][b_ds[j] + 1] = h2f((uint16_t)(br[j].d >> 16));
             if (TYPE == kQ5_1) {
@@ -582,9 +586,11 @@ __global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int m
     };
 
     // ---- weight loader: tile n of this wave is tile row wave * TN + n of the workgroup
+    // byte quants (see quant_rsrc), Q5_1 but in the 64 x 256 tile
+    constexpr bool BQ = TYPE == kQ8_0 || (TYPE == kQ5_1 && TM * TN < 16);
     rsrc_t rq[TN], rd[TN], rh[TN];
     int btile0[TN];
-    const uint32_t vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
+    const uint32_t vq = (uint32_t)lane * (BQ ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
 #pragma unroll
     for (int n = 0; n < TN; n++) {
         const int t = wave * TN + n;
@@ -608,9 +614,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int m
         const QWeight &w = a.seg[seg];
         const int KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
-        rq[n] = make_rsrc(w.qs, tiles * tile_qs_bytes(TYPE));
+        rq[n] = quant_rsrc<TYPE, BQ>(w, tiles);
         rd[n] = make_rsrc(w.d, tiles * tile_d_bytes(TYPE));
-        if (TYPE == kQ5_1) rh[n] = make_rsrc(w.qh, tiles * 128);
+        if (TYPE == kQ5_1 && !BQ) rh[n] = make_rsrc(w.qh, tiles * 128);
         btile0[n] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + (kb_begin >> 1));
     }
     auto load_b = [&](int st, BChunk (&br)[TN]) __attribute__((always_inline)) {
@@ -618,7 +624,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int m
 #pragma unroll
         for (int n = 0; n < TN; n++) {
             const int tile = btile0[n] + st;
-            if (TYPE == kQ8_0) {
+            if (BQ) {
                 br[n].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[n], vq, tile * 1024, 0));
             } else {
                 uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[n], vq, tile * 512, 0));
@@ -628,7 +634,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int m
                 const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[n], 2 * vd, tile * 128, 0));
                 br[n].d = dm.x;
                 br[n].m = dm.y;
-                br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
+                if (!BQ) br[n].qh = __builtin_amdgcn_raw_buffer_load_b16(rh[n], vh, tile * 128, 0);
             } else {
                 br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
             }
@@ -688,7 +694,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void gemm_bd_kernel(GemmArgs a, int m
             float dv[TN], mv[TN];
 #pragma unroll
             for (int n = 0; n < TN; n++) {
-                bf[n] = decode_b_frag<TYPE>(br[n], bb);
+                bf[n] = decode_b_frag<TYPE, BQ>(br[n], bb);
                 dv[n] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d))) & live);
                 if (TYPE == kQ5_1)
                     mv[n] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].m >> 16 : br[n].m))) & live);
@@ -871,7 +877,7 @@ template <int TYPE, int MODE, int U, int CH>
 __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngroups, int nq)
 {
     constexpr int TN = MODE == kGemmSwiGlu ? 2 : 1;
-    constexpr int NB = (TYPE == kQ5_1 ? 3 : 2) * TN; // weight loads per stage
+    constexpr int NB = 2 * TN; // weight loads per stage
     static_assert(CH % U == 0, "ring slots restart at every chunk");
     static_assert(CH * NB + CH + 1 <= 63, "outstanding loads beyond the vmcnt range");
     __shared__ __attribute__((aligned(16))) uint4 As[2][CH * 4 * 64]; // [stage][block][part][lane]
@@ -897,10 +903,11 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
     if (TYPE == kQ5_1) rs = make_rsrc(a.xsum, (uint32_t)M * nblk * 4);
 
     // weights: tile n of this wave
-    rsrc_t rq[TN], rd[TN], rh[TN];
+    constexpr bool BQ = TYPE != kQ4_0; // byte quants (see quant_rsrc)
+    rsrc_t rq[TN], rd[TN];
     int btile0[TN];
     int seg_store = 0, start_store = 0;
-    const uint32_t vq = (uint32_t)lane * (TYPE == kQ8_0 ? 16 : 8), vd = 4 * (lane & 15), vh = 2 * lane;
+    const uint32_t vq = (uint32_t)lane * (BQ ? 16 : 8), vd = 4 * (lane & 15);
 #pragma unroll
     for (int n = 0; n < TN; n++) {
         int seg, rgw;
@@ -922,9 +929,8 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
         const QWeight &wt = a.seg[seg];
         const int KP = tile_kpairs(wt.cols), RG = tile_rows(wt.rows);
         const uint32_t tiles = (uint32_t)RG * KP;
-        rq[n] = make_rsrc(wt.qs, tiles * tile_qs_bytes(TYPE));
+        rq[n] = quant_rsrc<TYPE, BQ>(wt, tiles);
         rd[n] = make_rsrc(wt.d, tiles * tile_d_bytes(TYPE));
-        if (TYPE == kQ5_1) rh[n] = make_rsrc(wt.qh, tiles * 128);
         btile0[n] = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP + (kb_begin >> 1));
     }
     auto load_b = [&](int st, BChunk (&br)[TN]) __attribute__((always_inline)) {
@@ -932,7 +938,7 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
 #pragma unroll
         for (int n = 0; n < TN; n++) {
             const int tile = __builtin_amdgcn_readfirstlane(btile0[n] + st);
-            if (TYPE == kQ8_0) {
+            if (BQ) {
                 br[n].q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq[n], vq, tile * 1024, 0));
             } else {
                 uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq[n], vq, tile * 512, 0));
@@ -942,11 +948,6 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
                 const uint2 dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd[n], 2 * vd, tile * 128, 0));
                 br[n].d = dm.x;
                 br[n].m = dm.y;
-                // the aligned word holding the lane's two bytes, shifted where
-                // it is decoded: a 16-bit load's zero-extension is an
-                // instruction the compiler hoists into an earlier stage, where
-                // it waits on the whole ring behind it
-                br[n].qh = __builtin_amdgcn_raw_buffer_load_b32(rh[n], vh & ~3u, tile * 128, 0);
             } else {
                 br[n].d = __builtin_amdgcn_raw_buffer_load_b32(rd[n], vd, tile * 64, 0);
             }
@@ -996,9 +997,7 @@ __global__ __launch_bounds__(256, 2) void gemm_skinny_kernel(GemmArgs a, int ngr
             if (TYPE == kQ5_1) xs4 = *(const floatx4 *)&Xs[buf][(sl * 2 + bb) * 16 + 4 * (lane >> 4)];
 #pragma unroll
             for (int n = 0; n < TN; n++) {
-                BChunk c = br[n];
-                if (TYPE == kQ5_1) c.qh >>= 8 * (vh & 2); // odd lanes: the word's high half
-                const half8_t bf = decode_b_frag<TYPE>(c, bb);
+                const half8_t bf = decode_b_frag<TYPE, BQ>(br[n], bb);
                 const float dv = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h2f((uint16_t)(bb ? br[n].d >> 16 : br[n].d))) & live);
                 float mv = 0.f;
                 if (TYPE == kQ5_1)

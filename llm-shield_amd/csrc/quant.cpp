@@ -100,7 +100,7 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 QLayout qlayout(int type, int64_t rows, int64_t cols)
 {
-    QLayout l{0, 0, 0, 0, 0};
+    QLayout l{0, 0, 0, 0, 0, 0};
     const size_t tiles = (size_t)tile_rows((int)rows) * (size_t)tile_kpairs((int)cols);
     l.qs = 0;
     l.d = align256(tiles * tile_qs_bytes(type));
@@ -109,6 +109,8 @@ QLayout qlayout(int type, int64_t rows, int64_t cols)
         l.m = l.d + 4; // interleaved with the scales: row r's mins at 8 r + 4
         l.qh = align256(end);
         end = l.qh + tiles * 128;
+        l.qb = align256(end);
+        end = l.qb + tiles * 1024;
     }
     l.total = align256(end);
     return l;
@@ -132,7 +134,10 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
         auto clear = [&](size_t off, size_t per_tile) { std::memset(out + off + g0 * KP * per_tile, 0, (g1 - g0) * KP * per_tile); };
         clear(L.qs, TQ);
         clear(L.d, (size_t)tile_d_bytes(type));
-        if (type == kQ5_1) clear(L.qh, 128);
+        if (type == kQ5_1) {
+            clear(L.qh, 128);
+            clear(L.qb, 1024);
+        }
     });
     parallel_rows(rows, threads, [&](int64_t r0, int64_t r1) {
         for (int64_t row = r0; row < r1; row++) {
@@ -166,7 +171,16 @@ bool repack_host(int type, int64_t rows, int64_t cols, const void *gguf, void *d
                         auto nib = [&](int j) { return j < 16 ? (qs[j] & 15) : (qs[j - 16] >> 4); };
                         dq[i] = (uint8_t)(nib(8 * g + i) | (nib(8 * g + i + 4) << 4));
                     }
-                    if (type == kQ5_1) out[L.qh + tile * 128 + 2 * (16 * g + r) + bb] = (uint8_t)((qh >> (8 * g)) & 0xffu);
+                    if (type == kQ5_1) {
+                        out[L.qh + tile * 128 + 2 * (16 * g + r) + bb] = (uint8_t)((qh >> (8 * g)) & 0xffu);
+                        // the byte copy: element 8 g + i at byte 8 bb + i of lane 16 g + r
+                        uint8_t *db = out + L.qb + tile * 1024 + 16 * (16 * g + r) + 8 * bb;
+                        for (int i = 0; i < 8; i++) {
+                            const int j = 8 * g + i;
+                            const int nibj = j < 16 ? (qs[j] & 15) : (qs[j - 16] >> 4);
+                            db[i] = (uint8_t)(nibj | (((qh >> j) & 1u) << 4));
+                        }
+                    }
                 }
             }
         }

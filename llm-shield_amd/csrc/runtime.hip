@@ -326,6 +326,7 @@ int upload_weight(int type, int64_t rows, int64_t cols, const void *bytes, QWeig
     w.d = (const uint16_t *)(b8 + L.d);
     w.m = type == kQ5_1 ? (const uint16_t *)(b8 + L.m) : nullptr;
     w.qh = type == kQ5_1 ? b8 + L.qh : nullptr;
+    w.qb = type == kQ5_1 ? b8 + L.qb : nullptr;
     return JEV_OK;
 }
 
