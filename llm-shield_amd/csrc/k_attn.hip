@@ -35,6 +35,8 @@
 // by the consumer, the O projection's GEMV, while it stages its input.
 #include "jev_dev.h"
 
+#include <type_traits>
+
 namespace jev {
 
 namespace {
@@ -48,10 +50,20 @@ __device__ __forceinline__ int swz(int key) { return ((key & 3) << 2) | ((key >>
 typedef short short4_t __attribute__((ext_vector_type(4)));
 // ds_read_b64_tr_b16 over a 16-lane group: lane 4 a + e receives element e of
 // the 8 bytes addressed by lanes a, a + 4, a + 8, a + 12 (in that order).
-__device__ __forceinline__ uint2 read_tr(const char *p)
+__device__ __forceinline__ uint2 read_tr(uint32_t lds_byte)
 {
-    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)p);
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)(size_t)lds_byte);
     return __builtin_bit_cast(uint2, v);
+}
+
+// LDS byte address of a __shared__ object, and a 16-byte read at one.
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p;
+}
+__device__ __forceinline__ half8_t lds_load8h(uint32_t lds_byte)
+{
+    return *(const __attribute__((address_space(3))) half8_t *)(size_t)lds_byte;
 }
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -82,14 +94,29 @@ __device__ __forceinline__ half8_t cat4(uint2 a, uint2 b)
 // head (blockIdx.z); each stages the blocks and computes the scores and
 // softmax (the same instructions on the same data) and accumulates 128 / DS
 // of the output dims.  Every output is the same chain of MFMAs either way.
+//
+// Schedule (one wave per SIMD: the workgroup's 128 KiB of LDS fills the CU):
+// a wave's matrix-core work and its softmax overlap only if its instruction
+// stream interleaves them, so each block is two regions of independent work:
+//   A(b): S(b) = K(b) Q^T on the matrix cores, beside the second half of block
+//         b - 1's softmax (row sum, P pairs, o *= alpha) on the vector ALU;
+//   B(b): O^T += V^T P^T of block b - 1 on the matrix cores, beside the first
+//         half of block b's softmax (mask, running max, exponentials).
+// The operations and their order per output are those of the plain sequence
+// S(b), P V(b - 1), softmax(b), rescale, so the bits do not depend on it.
 template <int DS>
 __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 {
     constexpr int ND = 4 / DS; // 32-dim output tiles per wave
     // Double-buffered K and V blocks as fp16 pairs: [key][hi, lo][16 chunks of
     // 8 dims], chunks swizzled per key (chunk ^ swz(key)) so that both the
-    // K fragment reads and the V transpose reads hit distinct banks.
-    __shared__ __attribute__((aligned(16))) uint4 Ks0[KCH], Vs0[KCH], Ks1[KCH], Vs1[KCH];
+    // K fragment reads and the V transpose reads hit distinct banks.  One
+    // array, K0 K1 V0 V1: a K read reaches its buffer through the LDS
+    // instruction's 16-bit offset, a V read from a base of 64 KiB held in
+    // its address register.
+    __shared__ __attribute__((aligned(16))) uint4 lds[4 * KCH];
+    uint4 *const Ks0 = lds, *const Ks1 = lds + KCH, *const Vs0 = lds + 2 * KCH, *const Vs1 = lds + 3 * KCH;
+    constexpr uint32_t KBUF = KCH * 16; // bytes per buffer
 
     // Longest tiles first: the plan lists tiles in token order, and later
     // tokens see more keys.
@@ -171,6 +198,9 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
             split4(v1, h1, l1);
             qh[c] = cat4(h0, h1);
             ql[c] = cat4(l0, l1);
+            // The Q fragments are only ever MFMA B operands: accumulation
+            // registers, leaving the vector registers to the softmax and P V.
+            asm volatile("" : "+a"(qh[c]), "+a"(ql[c]));
         }
     }
 
@@ -178,12 +208,13 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     // 2 c + g.  swz(32 t + col) = swz(col).
     uint32_t koff[8];
 #pragma unroll
-    for (int c = 0; c < 8; c++) koff[c] = col * 512 + ((2 * c + g) ^ swz(col)) * 16;
+    for (int c = 0; c < 8; c++) koff[c] = lds_addr(Ks0) + col * 512 + ((2 * c + g) ^ swz(col)) * 16;
     // V^T fragment (transpose reads): lane (G = lane / 16, s = lane % 16)
     // supplies key 16 c + 8 r + 4 (G / 2) + s / 4 at dims 32 d + 16 (G % 2) +
     // 4 (s % 4); it receives dim 32 d + lane % 32 of the four keys
-    // 16 c + 8 r + 4 (G / 2) + j.  Offsets for c = 0, hi part; c adds 16 keys.
-    uint32_t voff[2][4];
+    // 16 c + 8 r + 4 (G / 2) + j.  Addresses for c = 0, hi part, buffer V0; c
+    // adds 16 keys.  Kept opaque so the V0 base stays in the register.
+    uint32_t vadr[2][4];
     {
         const int s16 = lane & 15, G = lane >> 4, gp = G >> 1;
 #pragma unroll
@@ -192,7 +223,8 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
             for (int d = 0; d < 4; d++) {
                 const int key = 8 * r + 4 * gp + (s16 >> 2);
                 const int lc = 4 * d + 2 * (G & 1) + ((s16 & 3) >> 1);
-                voff[r][d] = key * 512 + ((lc ^ swz(key)) * 16) + 8 * (s16 & 1);
+                vadr[r][d] = lds_addr(Vs0) + key * 512 + ((lc ^ swz(key)) * 16) + 8 * (s16 & 1);
+                asm volatile("" : "+v"(vadr[r][d]));
             }
     }
 
@@ -202,148 +234,193 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 #pragma unroll
         for (int j = 0; j < 16; j++) o[d][j] = 0.f;
     float m_run = -INFINITY, l_run = 0.f; // running max in log2 units
-    // P of the previous block as pairs: chunk c's B fragments
-    half8_t pbh[4], pbl[4];
+    float alpha = 0.f;                    // exp2(previous max - new max) of the block in ex
+    floatx16 sc[2];                       // S^T of the block being scored
+    floatx16 ex[2];                       // exp2(s - max) of the block in the softmax
+    half8_t pbh[4], pbl[4];               // its P as pairs: chunk c's B fragments
 
-    // Iteration b: S(b) on the matrix cores, then block b's softmax on the
-    // vector ALUs while block b - 1's P V runs on the matrix cores.  Staged
-    // one iteration ahead: K(b + 1) and V(b).  K and V are double-buffered
-    // (K(b) in Kc, V(b - 1) in Vp; the loads go to Kn and Vn).
-    auto iter = [&](int b, const uint4 *Kc, const uint4 *Vp, uint4 *Kn, uint4 *Vn) __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's K(b) and V(b - 1) have landed
-        __syncthreads();                    // everyone's; K(b - 1) and V(b - 2) are free again
-        if (b + 1 < nblocks) stage(b + 1, kpb, Kn);
-        if (b < nblocks) stage(b, vpb, Vn);
-        if (!head_ok) return;
-        const bool live = b < nblocks;
-
-        floatx16 sc[2];
-        if (live) {
-            // S^T for the block's two 32-key halves; the K fragments of the
-            // step after next are read while this step's six MFMAs run.
-            const char *kb = (const char *)Kc;
-            half8_t kf[2][4];
-            auto kread = [&](int c, half8_t (&f)[4]) __attribute__((always_inline)) {
+    // S^T for the block in K buffer kb (byte offset 0 or KBUF), two 32-key
+    // halves.  Each K fragment of dim chunk c + 1 is read as soon as the last
+    // MFMA of chunk c that uses its register has issued.  slot(k) runs after
+    // the k-th of the 48 MFMAs, in a scheduling region of its own: the order
+    // written here is the order issued.
+    auto scores = [&](uint32_t kb, auto &&slot) __attribute__((always_inline)) {
+        half8_t kf[4]; // [2 t + part]
+        auto kread = [&](int c, int i) __attribute__((always_inline)) {
+            kf[i] = lds_load8h(koff[c] + kb + (i >> 1) * (32 * 512) + (i & 1) * 256);
+        };
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const char *kr = kb + t * (32 * 512) + koff[c];
-                    f[2 * t] = *(const half8_t *)kr;
-                    f[2 * t + 1] = *(const half8_t *)(kr + 256);
-                }
-            };
-            kread(0, kf[0]);
-            kread(1, kf[1]);
+        for (int i = 0; i < 4; i++) kread(0, i);
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const half8_t(&f)[4] = kf[c & 1];
+        for (int c = 0; c < 8; c++) {
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const floatx16 acc = c == 0 ? floatx16{} : sc[t];
-                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], qh[c], acc, 0, 0, 0);
-                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t], ql[c], sc[t], 0, 0, 0);
-                    sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * t + 1], qh[c], sc[t], 0, 0, 0);
-                }
-                if (c + 2 < 8) kread(c + 2, kf[c & 1]);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
-                if (c + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            for (int t = 0; t < 2; t++) {
+                const floatx16 acc = c == 0 ? floatx16{} : sc[t];
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * t], qh[c], acc, 0, 0, 0);
+                slot(6 * c + 3 * t);
+                __builtin_amdgcn_sched_barrier(0);
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * t], ql[c], sc[t], 0, 0, 0);
+                if (c + 1 < 8) kread(c + 1, 2 * t);
+                slot(6 * c + 3 * t + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[2 * t + 1], qh[c], sc[t], 0, 0, 0);
+                if (c + 1 < 8) kread(c + 1, 2 * t + 1);
+                slot(6 * c + 3 * t + 2);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+    };
 
-        // O^T += V^T P^T for block b - 1 over four 16-key chunks.  Chunk c's k
-        // slot 8 g + i is key 16 c + 8 (i / 4) + 4 g + i % 4: the P values
-        // sc[c / 2][8 (c % 2) + i] of this lane, split into pbh / pbl.
-        if (b >= 1) {
-            // 4 ND steps (chunk c, dim tile d); the V^T fragments of the
-            // step after next are read while this step's three MFMAs run
-            constexpr int NST = 4 * ND;
-            const char *vb = (const char *)Vp;
-            uint2 vf[3][4];
-            auto vread = [&](int st, uint2 (&f)[4]) __attribute__((always_inline)) {
-                const int c = st / ND, d = ND * dh + st % ND;
-                const char *v0 = vb + c * (16 * 512) + voff[0][d];
-                const char *v1 = vb + c * (16 * 512) + voff[1][d];
-                f[0] = read_tr(v0);
-                f[1] = read_tr(v1);
-                f[2] = read_tr(v0 + 256);
-                f[3] = read_tr(v1 + 256);
-            };
-            vread(0, vf[0]);
-            vread(1, vf[1]);
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                const int c = st / ND, d = st % ND;
-                if (st + 2 < NST) vread(st + 2, vf[(st + 2) % 3]);
-                const uint2(&f)[4] = vf[st % 3];
-                const half8_t vh = cat4(f[0], f[1]), vl = cat4(f[2], f[3]);
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbl[c], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, pbh[c], o[d], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
-#pragma unroll
-            for (int st = 0; st < NST; st++) {
-                if (st + 2 < NST) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 1);
-            }
+    // O^T += V^T P^T for the block in V buffer vb over four 16-key chunks,
+    // 4 ND steps (chunk c, dim tile d); the V^T fragments of the step after
+    // next are read while this step's three MFMAs run.  Chunk c's k slot
+    // 8 g + i is key 16 c + 8 (i / 4) + 4 g + i % 4: the P values
+    // ex[c / 2][8 (c % 2) + i] of this lane, as pbh / pbl.  slot(k) as above,
+    // after the k-th of the 12 ND MFMAs.
+    auto pv = [&](uint32_t vb, auto &&slot) __attribute__((always_inline)) {
+        constexpr int NST = 4 * ND;
+        // [step % 2][hi pair (two reads), lo pair]; a pair for step st + 2 is
+        // read as soon as step st's last MFMA using its registers has issued
+        uint2 vf[2][4];
+        auto vread = [&](int st, int half) __attribute__((always_inline)) {
+            const int c = st / ND, d = ND * dh + st % ND;
+            const uint32_t v0 = vadr[0][d] + vb + c * (16 * 512) + half * 256, v1 = vadr[1][d] + vb + c * (16 * 512) + half * 256;
+            vf[st & 1][2 * half] = read_tr(v0);
+            vf[st & 1][2 * half + 1] = read_tr(v1);
+        };
+        vread(0, 0);
+        vread(0, 1);
+        if (NST > 1) {
+            vread(1, 0);
+            vread(1, 1);
         }
-        if (!live) return;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const int c = st / ND, d = st % ND;
+            const uint2(&f)[4] = vf[st & 1];
+            const half8_t vh = cat4(f[0], f[1]), vl = cat4(f[2], f[3]);
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbh[c], o[d], 0, 0, 0);
+            slot(3 * st);
+            __builtin_amdgcn_sched_barrier(0);
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pbl[c], o[d], 0, 0, 0);
+            if (st + 2 < NST) vread(st + 2, 0);
+            slot(3 * st + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, pbh[c], o[d], 0, 0, 0);
+            if (st + 2 < NST) vread(st + 2, 1);
+            slot(3 * st + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
 
-        // Block b's softmax.  Where the block reaches past the tile's first
-        // query, mask by the logical key index.  sc[t][j] holds key
-        // 32 t + 8 (j / 4) + 4 g + j % 4.
-        if ((b + 1) * KB > min_limit) {
+    // Softmax of block b, first half, in the NS1 = 12 ND slots of P V: the
+    // mask (where the block reaches past the tile's first query, by logical
+    // key index), the running max, the exponentials.  sc[t][j] holds key
+    // 32 t + 8 (j / 4) + 4 g + j % 4.  PER slots' worth of work per slot.
+    constexpr int NS1 = 12 * ND, PER = 48 / NS1;
+    constexpr int MAX_SLOTS = 8 / PER, BPERM = MAX_SLOTS, MNEW = MAX_SLOTS + 1 + (PER == 1), EXP0 = MNEW + 1;
+    float bmax = -INFINITY, bmax_o = -INFINITY, m_new = 0.f;
+    auto soft1 = [&](int k, int b, auto masked) __attribute__((always_inline)) {
+        if (k < MAX_SLOTS) {
+            if (k == 0) bmax = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
+            for (int u = 4 * PER * k; u < 4 * PER * (k + 1); u++) {
+                const int t = u >> 4, j = u & 15;
+                if constexpr (decltype(masked)::value) {
                     const int kl = b * KB + 32 * t + 8 * (j >> 2) + 4 * g + (j & 3);
                     sc[t][j] = kl < my_limit ? sc[t][j] : -INFINITY;
                 }
-        }
-        float bmax = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int j = 0; j < 16; j++) bmax = fmaxf(bmax, sc[t][j]);
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        const float m_new = fmaxf(m_run, bmax);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        float psum = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int t = c >> 1, j0 = 8 * (c & 1);
-            float pv[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                pv[i] = __builtin_amdgcn_exp2f(sc[t][j0 + i] - m_new);
-                psum += pv[i];
+                bmax = fmaxf(bmax, sc[t][j]);
             }
-            uint2 ph0, pl0, ph1, pl1;
-            split4(make_float4(pv[0], pv[1], pv[2], pv[3]), ph0, pl0);
-            split4(make_float4(pv[4], pv[5], pv[6], pv[7]), ph1, pl1);
-            pbh[c] = cat4(ph0, ph1);
-            pbl[c] = cat4(pl0, pl1);
         }
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        // o * 1 is o: the rescale runs only when some row's max moved (after
-        // block b - 1's P V, before block b's)
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+        if (k == BPERM) bmax_o = __shfl_xor(bmax, 32, 64);
+        if (k == MNEW) {
+            m_new = fmaxf(m_run, fmaxf(bmax, bmax_o));
+            alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+        }
+        if (k >= EXP0 && k < EXP0 + 32 / PER) {
 #pragma unroll
-            for (int d = 0; d < ND; d++)
-#pragma unroll
-                for (int j = 0; j < 16; j++) o[d][j] = o[d][j] * alpha;
+            for (int u = PER * (k - EXP0); u < PER * (k - EXP0 + 1); u++)
+                ex[u >> 4][u & 15] = __builtin_amdgcn_exp2f(sc[u >> 4][u & 15] - m_new);
         }
     };
-    for (int b = 0; b <= nblocks; b += 2) {
-        iter(b, Ks0, Vs1, Ks1, Vs0);
-        if (b + 1 <= nblocks) iter(b + 1, Ks1, Vs0, Ks0, Vs1);
+    // Second half, in the 48 slots of the next block's S: the row sum (in key
+    // order), the P pairs, and the rescale of the output accumulated so far
+    // (o * 1 is o, so it runs unconditionally).
+    float psum = 0.f, psum_o = 0.f;
+    auto soft2 = [&](int k) __attribute__((always_inline)) {
+        if (k == 0) psum = 0.f;
+        if (k < 32) psum += ex[k >> 4][k & 15];
+        if (k % 3 == 0 && k / 3 < 16) {
+            // values u, u + 1 (u = 2 (k / 3)) into 32-bit part u / 2 % 4 of chunk u / 8
+            typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+            const int u = 2 * (k / 3), t = u >> 4, j = u & 15, c = u >> 3, part = (u >> 1) & 3;
+            const float x0 = ex[t][j], x1 = ex[t][j + 1];
+            const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+            const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(x0 - (float)h[0], x1 - (float)h[1]);
+            uint4 hv = __builtin_bit_cast(uint4, pbh[c]), lv = __builtin_bit_cast(uint4, pbl[c]);
+            (&hv.x)[part] = __builtin_bit_cast(uint32_t, h);
+            (&lv.x)[part] = __builtin_bit_cast(uint32_t, l);
+            pbh[c] = __builtin_bit_cast(half8_t, hv);
+            pbl[c] = __builtin_bit_cast(half8_t, lv);
+        }
+        if (k == 33) psum_o = __shfl_xor(psum, 32, 64);
+        if (k == 36) l_run = l_run * alpha + (psum + psum_o);
+#pragma unroll
+        for (int e = (k * 16 * ND + 47) / 48; e < ((k + 1) * 16 * ND + 47) / 48; e++) o[e >> 4][e & 15] *= alpha;
+    };
+    auto none = [](int) {};
+    using Plain = std::integral_constant<bool, false>;
+    using Masked = std::integral_constant<bool, true>;
+    // block b reaches past the tile's first query: its scores need the mask
+    auto tail = [&](int b) { return (b + 1) * KB > min_limit; };
+
+    // Block 0: staged K(1) and V(0), S(0) and its softmax's first half.
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): this thread's K(0) has landed
+    __syncthreads();                    // everyone's
+    if (nblocks > 1) stage(1, kpb, Ks1);
+    stage(0, vpb, Vs0);
+    // A wave past the group's last head (group not a multiple of 4) computes
+    // its clamped head's rows like the others and stores nothing: no branch
+    // around the block loop, so every block keeps o, sc and ex in place.
+    scores(0, none);
+    if (tail(0)) {
+#pragma unroll
+        for (int k = 0; k < NS1; k++) soft1(k, 0, Masked{});
+    } else {
+#pragma unroll
+        for (int k = 0; k < NS1; k++) soft1(k, 0, Plain{});
     }
+    // Block b >= 1: K(b) in buffer b % 2, V(b - 1) in the other; K(b + 1) and
+    // V(b) are staged while A(b) and B(b) run.
+    auto step = [&](int b, uint32_t kb, uint32_t vb, uint4 *Kn, uint4 *Vn, auto masked) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0x0F70); // this thread's K(b) and V(b - 1) have landed
+        __syncthreads();                    // everyone's; K(b - 1) and V(b - 2) are free again
+        if (b + 1 < nblocks) stage(b + 1, kpb, Kn);
+        stage(b, vpb, Vn);
+        __builtin_amdgcn_sched_barrier(0);
+        scores(kb, soft2);
+        pv(vb, [&](int k) __attribute__((always_inline)) { soft1(k, b, masked); });
+    };
+    for (int b = 1; b < nblocks; b += 2) {
+        if (tail(b))
+            step(b, KBUF, 0, Ks0, Vs1, Masked{});
+        else
+            step(b, KBUF, 0, Ks0, Vs1, Plain{});
+        if (b + 1 < nblocks) {
+            if (tail(b + 1))
+                step(b + 1, 0, KBUF, Ks1, Vs0, Masked{});
+            else
+                step(b + 1, 0, KBUF, Ks1, Vs0, Plain{});
+        }
+    }
+    // The last block's second softmax half and P V.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 48; k++) soft2(k);
+    pv(((nblocks - 1) & 1) ? KBUF : 0, none);
 
     if (q_ok) {
         // o[d][j] is dim 32 (ND dh + d) + 8 (j / 4) + 4 g + j % 4: four
