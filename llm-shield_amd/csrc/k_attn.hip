@@ -56,6 +56,19 @@ __device__ __forceinline__ uint2 read_tr(uint32_t lds_byte)
     return __builtin_bit_cast(uint2, v);
 }
 
+// x - (float)h for h the low (hi_half = false) or high fp16 of `h2`, by one
+// v_fma_mix_f32 (h * -1 + x, the f16 source converted exactly): the same
+// bits as converting h and subtracting, fp16 denormals included.
+__device__ __forceinline__ float pair_rem(uint32_t h2, float x, bool hi_half)
+{
+    float r;
+    if (hi_half)
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(x));
+    return r;
+}
+
 // LDS byte address of a __shared__ object, and a 16-byte read at one.
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
@@ -130,8 +143,6 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     const bool head_ok = hl < a.group;              // wave-uniform
     const int head = kvh * a.group + min(hl, a.group - 1);
     const int qdim = a.n_heads * 128;
-    const char *kpb = (const char *)(a.kp + (size_t)kvh * a.cap * 256);
-    const char *vpb = (const char *)(a.vp + (size_t)kvh * a.cap * 256);
 
     const int n_sh = tile.shared_hi - tile.shared_lo;
     // This lane's query is column `col` of S^T / O^T; lanes col and col + 32
@@ -156,29 +167,33 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
         skey[i] = 16 * wave + 2 * i + (lane >> 5);
         soff[i] = skey[i] * 512 + ((lane >> 4) & 1) * 256 + ((lane & 15) ^ swz(skey[i])) * 16;
     }
-    // One block of 64 logical keys from `src` into `dst`.  A block inside one
-    // contiguous range below the last visible key has slot = base + key: a
-    // uniform address plus the lane's constant offset.
-    auto stage = [&](int b, const char *src, uint4 *dst) __attribute__((always_inline)) {
+    // One block of 64 logical keys from `src` (the KV head's pair rows) into
+    // `dst`.  A block inside one contiguous range below the last visible key
+    // has slot = base + key: a uniform offset plus the lane's constant one.
+    // Buffer loads straight to LDS: as loads they count on the vector-memory
+    // counter alone, so the LDS reads after them wait for exactly the reads
+    // they need.
+    auto stage = [&](int b, rsrc_t src, uint4 *dst) __attribute__((always_inline)) {
         const int k0 = b * KB;
         const bool in_shared = k0 + KB <= n_sh, in_seg = k0 >= n_sh;
         if (k0 + KB <= max_limit && (in_shared || in_seg)) {
             const int base = (in_shared ? tile.shared_lo + k0 : tile.segment + (k0 - n_sh));
-            const char *sb = src + (size_t)base * 512;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                __builtin_amdgcn_global_load_lds(sb + soff[i], (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64],
-                                                 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64], 16,
+                                                         soff[i], base * 512, 0, 0);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int kl = min(k0 + skey[i], max_limit - 1);
                 const uint32_t off = (uint32_t)slot_of(kl) * 512 + (soff[i] - skey[i] * 512);
-                __builtin_amdgcn_global_load_lds(src + off, (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64],
-                                                 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void *)&dst[(8 * wave + i) * 64], 16,
+                                                         off, 0, 0, 0);
             }
         }
     };
+    const rsrc_t kpb = make_rsrc(a.kp + (size_t)kvh * a.cap * 256, (uint32_t)a.cap * 512);
+    const rsrc_t vpb = make_rsrc(a.vp + (size_t)kvh * a.cap * 256, (uint32_t)a.cap * 512);
     stage(0, kpb, Ks0); // in flight while Q is read
 
     // Q^T fragments: dims 16 c + 8 g .. + 7 of this lane's query, scaled by
@@ -347,28 +362,36 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
     };
     // Second half, in the 48 slots of the next block's S: the row sum (in key
     // order), the P pairs, and the rescale of the output accumulated so far
-    // (o * 1 is o, so it runs unconditionally).
+    // (o * 1 is o, so it runs unconditionally).  Per three slots: one pair of
+    // P values split (over two slots), three row-sum terms, 4 ND / 4 output
+    // multiplies (two in the third slot): at most four vector instructions
+    // beside each MFMA, about what one wave issues while its MFMA runs.
     float psum = 0.f, psum_o = 0.f;
+    uint32_t p_hi = 0; // the pair in flight: its hi half
     auto soft2 = [&](int k) __attribute__((always_inline)) {
+        typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+        const int u = 2 * (k / 3), t = u >> 4, j = u & 15, c = u >> 3, part = (u >> 1) & 3;
         if (k == 0) psum = 0.f;
         if (k < 32) psum += ex[k >> 4][k & 15];
-        if (k % 3 == 0 && k / 3 < 16) {
-            // values u, u + 1 (u = 2 (k / 3)) into 32-bit part u / 2 % 4 of chunk u / 8
-            typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-            const int u = 2 * (k / 3), t = u >> 4, j = u & 15, c = u >> 3, part = (u >> 1) & 3;
-            const float x0 = ex[t][j], x1 = ex[t][j + 1];
-            const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
-            const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(x0 - (float)h[0], x1 - (float)h[1]);
-            uint4 hv = __builtin_bit_cast(uint4, pbh[c]), lv = __builtin_bit_cast(uint4, pbl[c]);
-            (&hv.x)[part] = __builtin_bit_cast(uint32_t, h);
-            (&lv.x)[part] = __builtin_bit_cast(uint32_t, l);
+        if (k % 3 == 0) {
+            p_hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(ex[t][j], ex[t][j + 1]));
+            uint4 hv = __builtin_bit_cast(uint4, pbh[c]);
+            (&hv.x)[part] = p_hi;
             pbh[c] = __builtin_bit_cast(half8_t, hv);
+        }
+        if (k % 3 == 1) {
+            // lo = the remainders x - hi (exact), rounded toward zero as hi was
+            const fp16x2 l = __builtin_amdgcn_cvt_pkrtz(pair_rem(p_hi, ex[t][j], false), pair_rem(p_hi, ex[t][j + 1], true));
+            uint4 lv = __builtin_bit_cast(uint4, pbl[c]);
+            (&lv.x)[part] = __builtin_bit_cast(uint32_t, l);
             pbl[c] = __builtin_bit_cast(half8_t, lv);
         }
         if (k == 33) psum_o = __shfl_xor(psum, 32, 64);
         if (k == 36) l_run = l_run * alpha + (psum + psum_o);
+        // output multiplies: weights 1, 1, 2 per three slots, 16 ND in all
+        auto mark = [](int kk) { return (16 * ND * (4 * (kk / 3) + (kk % 3))) / 64; };
 #pragma unroll
-        for (int e = (k * 16 * ND + 47) / 48; e < ((k + 1) * 16 * ND + 47) / 48; e++) o[e >> 4][e & 15] *= alpha;
+        for (int e = mark(k); e < mark(k + 1); e++) o[e >> 4][e & 15] *= alpha;
     };
     auto none = [](int) {};
     using Plain = std::integral_constant<bool, false>;
@@ -444,7 +467,9 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 {
     if (a.n_tiles <= 0) return hipSuccess;
-    if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp) return hipErrorInvalidValue;
+    // cap * 512 bytes per KV head is a buffer resource's 32-bit extent
+    if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp || a.cap <= 0 || a.cap > (1 << 23))
+        return hipErrorInvalidValue;
     const int n_kv = a.n_heads / a.group, hsets = (a.group + 3) / 4;
     const dim3 grid(n_kv * hsets, a.n_tiles);
     // fewer workgroups than compute units: the output dims split over two or four
