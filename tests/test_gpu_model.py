@@ -291,6 +291,29 @@ def test_projection_segments_off_the_wide_tile_grid(gpu, t, n):
     m.close()
 
 
+@pytest.mark.parametrize("heads,kv", [(6, 1), (10, 2)])
+@pytest.mark.parametrize("n", [70, 300])
+def test_query_groups_wider_than_four_heads(gpu, heads, kv, n):
+    # An attention workgroup serves four query heads of one KV head; a group of
+    # 5 or 6 heads takes two workgroups per KV head, the second with waves past
+    # the group's last head (they compute a clamped head and store nothing).
+    cfg = tiny_config(n_heads=heads, n_kv_heads=kv, initial_kv_capacity=1024)
+    synth = jev.SynthModel(cfg, jev.TYPE_Q8_0)
+    m = synth.open(0)
+    r = oracle.OracleModel(cfg).bind_synth(synth)
+    tokens = jev.random_tokens(n, 2048, n + heads)
+    assert worst_close(r.forward(tokens), m.forward(tokens)) <= 1e-3
+    m.reset_kv_cache()
+    r.reset_kv_cache()
+    trunk = jev.random_tokens(n // 2, 2048, 3)
+    branches = [jev.random_tokens(k, 2048, 40 + k) for k in (9, 33, 70)]
+    rows = [5, 1999]
+    got = np.array(m.forward_tree(trunk, branches, rows))
+    exp = np.array(r.forward_tree(trunk, branches, rows))
+    assert worst_close(exp, got) <= 1e-3
+    m.close()
+
+
 # ---------------------------------------------------------------- error paths
 
 def test_errors_match_reference_exceptions(model):
