@@ -22,9 +22,10 @@
 //
 // Operands are fp16 pairs (x = hi + lo, ~22 bits): every product is three
 // v_mfma_f32_32x32x16_f16 (hi.hi + hi.lo + lo.hi), which keeps fp32-grade
-// scores at a fraction of the fp32-MFMA cost.  The KV cache stays fp32; K and V
-// blocks are split into pairs while being staged in LDS, K as [key][dim] and V
-// transposed to [dim][key] so both operand fragments are vector reads.
+// scores at a fraction of the fp32-MFMA cost.  The KV cache stays fp32 and
+// carries fp16-pair shadows of every row ([hi, lo][dim], written with the
+// row); the kernel stages those shadows straight into LDS, where K fragments
+// are plain reads and V^T fragments transposing reads (ds_read_b64_tr_b16).
 //
 //   S^T (32 keys x 32 queries) = K (32 x 128) . Q^T      24 MFMAs per 32 keys
 //   O^T (128 x 32) += V^T (128 x 64) . P^T (64 x 32)      48 MFMAs per 64 keys,
