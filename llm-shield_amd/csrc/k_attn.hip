@@ -468,8 +468,9 @@ __global__ __launch_bounds__(256, 1) void attn_tree_kernel(AttnArgs a)
 hipError_t launch_attn_tree(const AttnArgs &a, hipStream_t s)
 {
     if (a.n_tiles <= 0) return hipSuccess;
-    // cap * 512 bytes per KV head is a buffer resource's 32-bit extent
-    if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp || a.cap <= 0 || a.cap > (1 << 23))
+    // cap * 512 bytes per KV head is a buffer resource's 32-bit extent (2^32
+    // itself would wrap to an empty resource)
+    if (a.hd != 128 || a.group < 1 || a.n_tiles > 65535 || !a.kp || !a.vp || a.cap <= 0 || a.cap >= (1 << 23))
         return hipErrorInvalidValue;
     const int n_kv = a.n_heads / a.group, hsets = (a.group + 3) / 4;
     const dim3 grid(n_kv * hsets, a.n_tiles);
