@@ -75,11 +75,13 @@ def test_gpu_matmul_matches_oracle(gpu, t, rows, cols, tokens):
 
 
 @pytest.mark.parametrize("t", [jev.TYPE_Q4_0, jev.TYPE_Q5_1, jev.TYPE_Q8_0])
-def test_gpu_matmul_batch_invariance_bitwise(gpu, t):
+@pytest.mark.parametrize("rows,cols", [(384, 3072), (200, 1056)])
+def test_gpu_matmul_batch_invariance_bitwise(gpu, t, rows, cols):
     # A token's result does not depend on its batch (PanelGemmTests.cs:61-74),
     # across the M tile boundary (128) too.
     # Small-M and large-M calls take different tile shapes; bits must not move.
-    rows, cols = 384, 3072
+    # 200 x 1056: a weight that ends inside a 32-row group, 33 quant blocks
+    # (an odd block count in the last K split).
     raw = jev.synth_tensor("inv", t, rows, cols)
     x = np.random.default_rng(1).standard_normal((700, cols)).astype(np.float32)
     full = matmul_gpu(t, raw, rows, cols, x, 700)
