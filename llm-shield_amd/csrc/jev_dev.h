@@ -27,7 +27,6 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // x ~= hi + lo with both halves fp16 (round to nearest even each time).
 __device__ __forceinline__ void split_f16(float x, uint16_t &hi, uint16_t &lo)
