@@ -18,6 +18,8 @@
 // sum is corrected by 8 * sum(q) (exact); Q5_1's 0..31 enter as they are.
 #include "jev_dev.h"
 
+#include <type_traits>
+
 namespace jev {
 
 namespace {
@@ -73,18 +75,120 @@ hipError_t launch_quant_act(const QuantActArgs &a, hipStream_t s)
 }
 
 // Wave w of workgroup (x, y) owns weight row group 4 x + w (16 output
-// columns) and the TM token groups from TM y.  No LDS, no barriers.
+// columns) and the TM token groups from TM y.  The activation side of a tile
+// pair (two quant blocks) -- the token groups' int8 fragments and their
+// per-block scale terms -- is the same for the workgroup's four waves, so it
+// is staged in LDS once per workgroup, CH pairs at a time, double buffered
+// with one barrier per chunk: loaded into registers a chunk ahead, written to
+// the free buffer at the end of the chunk.  Each wave streams its own weight
+// slots through a register ring DEPTH pairs ahead (buffer loads, the pair in
+// the scalar offset).  Loads past the last pair are clamped; the last chunk
+// discards what lies past the last block by selects, so each output takes its
+// blocks ascending, one IntegerDot step each.
 template <int TYPE, int TM>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args a)
+__global__ __launch_bounds__(256, 2) void gemm_i8_kernel(GemmI8Args a)
 {
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int CH = 8 / TM;             // tile pairs per staged chunk
+    constexpr int DEPTH = CH < 4 ? CH : 4; // weight ring (divides CH)
+    constexpr int NB = 2 * CH;             // blocks per chunk
+    constexpr bool AUX = TYPE != kQ8_0;    // Q4_0: quant sums; Q5_1: d * sum(q)
+    __shared__ __attribute__((aligned(16))) uint8_t sa[2][TM][NB][512]; // int8 fragments
+    __shared__ __attribute__((aligned(16))) float sd[2][TM][NB][16];    // x scales
+    __shared__ __attribute__((aligned(16))) float sx[2][TM][AUX ? NB : 1][16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, rl = lane & 15;
     const QWeight &w = a.w;
-    const int rgw = blockIdx.x * 4 + wave;
-    if (rgw * 16 >= w.rows) return; // wave-uniform
-    const int nb = w.cols >> 5, KP = tile_kpairs(w.cols);
+    const int nb = w.cols >> 5, KP = tile_kpairs(w.cols), RG = tile_rows(w.rows);
     const int tg0 = blockIdx.y * TM;
-    const size_t tile0 = (size_t)rgw * KP;
+    // waves past the weight's rows keep loading a clamped row group (their
+    // outputs are not stored): every wave reaches every barrier
+    const int rgw = blockIdx.x * 4 + wave;
+    const int tile0 = __builtin_amdgcn_readfirstlane(min(rgw, RG - 1) * KP);
+    const uint32_t tiles = (uint32_t)RG * KP;
+    constexpr bool BYTES = TYPE == kQ8_0;
+    const rsrc_t rq = make_rsrc(w.qs, tiles * (BYTES ? 1024u : 512u));
+    const rsrc_t rd = make_rsrc(w.d, tiles * (uint32_t)tile_d_bytes(TYPE));
+    rsrc_t rh;
+    if (TYPE == kQ5_1) rh = make_rsrc(w.qh, tiles * 128u);
+    const rsrc_t rx = make_rsrc(a.xq, (uint32_t)a.T16 * nb * 32u);
+    const rsrc_t rxd = make_rsrc(a.xd, (uint32_t)a.T16 * nb * 4u);
+    rsrc_t raux;
+    if (TYPE == kQ4_0) raux = make_rsrc(a.xqs, (uint32_t)a.T16 * nb * 4u);
+    if (TYPE == kQ5_1) raux = make_rsrc(a.xs, (uint32_t)a.T16 * nb * 4u);
+    const int nchunk = (KP + CH - 1) / CH;
+
+    // ---- activation chunk c: per token group, NB fragments of 512 B (16
+    // bytes per thread per pair of fragments) and NB x 16 scale terms (one
+    // float per thread per group of 16 blocks)
+    constexpr int AQ = TM * NB * 512 / 16 / 256; // 16-byte loads per thread
+    constexpr int AS = (TM * NB * 16 + 255) / 256; // scale floats per thread
+    struct AChunk {
+        uint4 q[AQ];
+        float d[AS], x[AS];
+    };
+    auto load_a = [&](int c, AChunk &r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < AQ; i++) {
+            const int e = i * 256 + tid;             // 16-byte element of the chunk
+            const int tm = e / (NB * 32), rem = e % (NB * 32);
+            const int lb = rem >> 5, part = rem & 31;  // block of the chunk, 16 bytes of its 512
+            const int kb = min(c * NB + lb, nb - 1);
+            const int tg = tg0 + tm;
+            // (the block varies per lane: all of it in the lane offset)
+            r.q[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)(tg * nb + kb) * 32 + part) * 16, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < AS; i++) {
+            const int e = min(i * 256 + tid, TM * NB * 16 - 1);
+            const int tm = e / (NB * 16), rem = e % (NB * 16);
+            const int lb = rem >> 4, t = rem & 15;
+            const int kb = min(c * NB + lb, nb - 1);
+            const uint32_t off = ((uint32_t)kb * a.T16 + 16 * (tg0 + tm) + t) * 4;
+            r.d[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rxd, off, 0, 0));
+            if (AUX) r.x[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(raux, off, 0, 0));
+        }
+    };
+    auto store_a = [&](int buf, const AChunk &r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < AQ; i++) {
+            const int e = i * 256 + tid;
+            const int tm = e / (NB * 32), rem = e % (NB * 32);
+            *(uint4 *)&sa[buf][tm][rem >> 5][16 * (rem & 31)] = r.q[i];
+        }
+#pragma unroll
+        for (int i = 0; i < AS; i++) {
+            const int e = i * 256 + tid;
+            if (e < TM * NB * 16) {
+                const int tm = e / (NB * 16), rem = e % (NB * 16);
+                sd[buf][tm][rem >> 4][rem & 15] = r.d[i];
+                if (AUX) sx[buf][tm][rem >> 4][rem & 15] = r.x[i];
+            }
+        }
+    };
+
+    // ---- weight slot of tile pair kp (clamped past the last)
+    struct WStage {
+        uint4 q;     // Q8_0 16 bytes, nibbles 8 in .x, .y
+        uint32_t qh; // Q5_1 fifth bits (block 0 low byte)
+        uint2 dm;    // two scales (.x; Q5_1: mins in .y)
+    };
+    auto load_w = [&](WStage &s, int kp) __attribute__((always_inline)) {
+        kp = min(kp, KP - 1);
+        const int tile = tile0 + kp;
+        if (BYTES) {
+            s.q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * lane, tile * 1024, 0));
+        } else {
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, 8 * lane, tile * 512, 0));
+            s.q = make_uint4(v.x, v.y, 0u, 0u);
+        }
+        if (TYPE == kQ5_1) {
+            s.qh = __builtin_amdgcn_raw_buffer_load_b16(rh, 2 * lane, tile * 128, 0);
+            s.dm = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rd, 8 * rl, tile * 128, 0));
+        } else {
+            s.dm.x = __builtin_amdgcn_raw_buffer_load_b32(rd, 4 * rl, tile * 64, 0);
+        }
+    };
 
     float acc[TM][4], off[TM][4];
 #pragma unroll
@@ -92,25 +196,24 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args a)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[mi][r] = off[mi][r] = 0.0f;
 
-    for (int kp = 0; kp < KP; kp++) {
-        const size_t tile = tile0 + kp;
+    // pair kp from LDS buffer buf (its blocks at lb0, lb0 + 1 of the chunk);
+    // CHECK: the pair may be the last (an odd block count's missing second
+    // block) or past it -- every earlier pair is whole and takes no selects
+    auto compute = [&](const WStage &s, int kp, int buf, int lb0, auto check) __attribute__((always_inline)) {
+        constexpr bool CHECK = decltype(check)::value;
         uint32_t wq[2][2]; // [block][dword]: the lane's 8 quants of each block
-        float dw[2], mw[2] = {0.0f, 0.0f};
         if (TYPE == kQ8_0) {
-            const uint4 q = *(const uint4 *)(w.qs + tile * 1024 + 16 * lane);
-            wq[0][0] = q.x ^ 0x80808080u;
-            wq[0][1] = q.y ^ 0x80808080u;
-            wq[1][0] = q.z ^ 0x80808080u;
-            wq[1][1] = q.w ^ 0x80808080u;
+            wq[0][0] = s.q.x ^ 0x80808080u;
+            wq[0][1] = s.q.y ^ 0x80808080u;
+            wq[1][0] = s.q.z ^ 0x80808080u;
+            wq[1][1] = s.q.w ^ 0x80808080u;
         } else {
-            const uint2 q = *(const uint2 *)(w.qs + tile * 512 + 8 * lane);
-            const uint32_t qh = TYPE == kQ5_1 ? *(const uint16_t *)(w.qh + tile * 128 + 2 * lane) : 0u;
 #pragma unroll
             for (int bb = 0; bb < 2; bb++) {
-                const uint32_t v = bb ? q.y : q.x;
+                const uint32_t v = bb ? s.q.y : s.q.x;
                 uint32_t n0 = v & 0x0f0f0f0fu, n1 = (v >> 4) & 0x0f0f0f0fu;
                 if (TYPE == kQ5_1) {
-                    const uint32_t hb = (qh >> (8 * bb)) & 0xffu;
+                    const uint32_t hb = (s.qh >> (8 * bb)) & 0xffu;
                     n0 |= (((hb & 15u) * 0x00204081u) & 0x01010101u) << 4;
                     n1 |= (((hb >> 4) * 0x00204081u) & 0x01010101u) << 4;
                 }
@@ -120,38 +223,67 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(GemmI8Args a)
         }
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
-            dw[bb] = h2f(TYPE == kQ5_1 ? w.d[tile * 64 + 4 * rl + bb] : w.d[tile * 32 + 2 * rl + bb]);
-            if (TYPE == kQ5_1) mw[bb] = h2f(w.d[tile * 64 + 4 * rl + 2 + bb]);
-        }
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            const int kb = 2 * kp + bb;
-            if (kb >= nb) break; // an odd block count's padding block does not exist
+            const bool valid = !CHECK || 2 * kp + bb < nb; // past the last block: the select keeps the sums
+            const float dw = h2f((uint16_t)(bb ? s.dm.x >> 16 : s.dm.x));
+            const float mw = TYPE == kQ5_1 ? h2f((uint16_t)(bb ? s.dm.y >> 16 : s.dm.y)) : 0.0f;
             const long bf = (long)(((uint64_t)wq[bb][1] << 32) | wq[bb][0]);
 #pragma unroll
             for (int mi = 0; mi < TM; mi++) {
-                const int tg = tg0 + mi;
-                const long af = *(const long *)(a.xq + (((size_t)tg * nb + kb) * 64 + lane) * 8);
+                const long af = *(const long *)&sa[buf][mi][lb0 + bb][8 * lane];
                 const int4v p = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, int4v{0, 0, 0, 0}, 0, 0, 0);
                 // this lane's outputs: tokens 16 tg + 4 g + r, column rl
-                const size_t bi = (size_t)kb * a.T16 + 16 * tg + 4 * g;
-                const float4 xd = *(const float4 *)(a.xd + bi);
+                const float4 xd = *(const float4 *)&sd[buf][mi][lb0 + bb][4 * g];
+                float4 xa = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (AUX) xa = *(const float4 *)&sx[buf][mi][lb0 + bb][4 * g];
                 const float xdv[4] = {xd.x, xd.y, xd.z, xd.w};
-                int4v xqs = {0, 0, 0, 0};
-                if (TYPE == kQ4_0) xqs = *(const int4v *)(a.xqs + bi);
-                float4 xs = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (TYPE == kQ5_1) xs = *(const float4 *)(a.xs + bi);
-                const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+                const float xav[4] = {xa.x, xa.y, xa.z, xa.w};
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int sumi = TYPE == kQ4_0 ? p[r] - 8 * xqs[r] : p[r];
-                    const float sc = dw[bb] * xdv[r];
-                    acc[mi][r] = acc[mi][r] + sc * (float)sumi;
-                    if (TYPE == kQ5_1) off[mi][r] = off[mi][r] + mw[bb] * xsv[r];
+                    const int sumi = TYPE == kQ4_0 ? p[r] - 8 * __builtin_bit_cast(int, xav[r]) : p[r];
+                    const float sc = dw * xdv[r];
+                    const float v = acc[mi][r] + sc * (float)sumi;
+                    acc[mi][r] = CHECK ? (valid ? v : acc[mi][r]) : v;
+                    if (TYPE == kQ5_1) {
+                        const float o = off[mi][r] + mw * xav[r];
+                        off[mi][r] = CHECK ? (valid ? o : off[mi][r]) : o;
+                    }
                 }
             }
         }
-    }
+    };
+
+    // ---- pipeline
+    AChunk ar;
+    WStage ring[DEPTH];
+    load_a(0, ar);
+#pragma unroll
+    for (int d = 0; d < DEPTH; d++) load_w(ring[d], d);
+    store_a(0, ar);
+    auto chunk = [&](int c, auto check) __attribute__((always_inline)) {
+        constexpr bool CHECK = decltype(check)::value;
+        const int buf = c & 1;
+        __syncthreads(); // chunk c staged by every wave; the other buffer is free
+        load_a(c + 1, ar); // past the last chunk: clamped reloads nobody reads
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int kp = c * CH + j;
+            if (!CHECK || kp < KP) compute(ring[j % DEPTH], kp, buf, 2 * j, check);
+            load_w(ring[j % DEPTH], kp + DEPTH);
+            // one pair at a time: the sums are taken here (left to the end of
+            // the chunk, every pair's products and scale terms stay live)
+#pragma unroll
+            for (int mi = 0; mi < TM; mi++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    asm volatile("" : "+v"(acc[mi][r]));
+                    if (TYPE == kQ5_1) asm volatile("" : "+v"(off[mi][r]));
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        store_a(buf ^ 1, ar);
+    };
+    for (int c = 0; c + 1 < nchunk; c++) chunk(c, std::false_type{});
+    chunk(nchunk - 1, std::true_type{});
 
     const int col = rgw * 16 + rl;
     if (col >= w.rows) return;
