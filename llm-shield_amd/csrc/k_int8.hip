@@ -37,9 +37,46 @@ __device__ __forceinline__ size_t xq_index(int t, int k, int nb)
 
 } // namespace
 
-// One 32-lane half-wave per (token, block).  Per-block results are stored
-// block-major ([b][t16]) so a lane reads its four output rows with one load.
+// Eight lanes per (token, block), four consecutive elements each (one
+// 16-byte load, one 4-byte store of quants).  The block's max |x| and its
+// integer quant sum are order-free, so any reduction tree gives the same
+// result.  Per-block results are stored block-major ([b][t16]) so a lane of
+// the GEMM reads its four output rows with one load.
 __global__ __launch_bounds__(256) void quant_act_kernel(QuantActArgs a)
+{
+    const int nb = a.K >> 5;
+    const int id = blockIdx.x * 32 + (threadIdx.x >> 3), i = threadIdx.x & 7;
+    if (id >= a.T * nb) return; // whole groups of eight; the shuffles stay inside them
+    const int t = id / nb, b = id % nb;
+    const float4 v = *(const float4 *)(a.x + (size_t)t * a.K + 32 * b + 4 * i);
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 8));
+    const float d = mx / 127.0f;
+    const float inverse = d != 0.0f ? 1.0f / d : 0.0f;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    int q[4], s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float scaled = vv[j] * inverse;
+        q[j] = min(127, max(-127, (int)roundf(scaled))); // roundf: half away from zero
+        s += q[j];
+    }
+#pragma unroll
+    for (int o = 4; o > 0; o >>= 1) s += __shfl_xor(s, o, 8);
+    // four consecutive k of one lane of the operand tile: contiguous bytes
+    *(uint32_t *)(a.xq + xq_index(t, 32 * b + 4 * i, nb)) =
+        (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) | ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
+    if (i == 0) {
+        const size_t bi = (size_t)b * a.T16 + t;
+        a.xd[bi] = (float)(_Float16)d; // the stored Half scale
+        a.xqs[bi] = s;
+        a.xs[bi] = d * (float)s; // QuantMatMul's block sums use the float d
+    }
+}
+
+// x not 16-byte aligned: one lane per element, the same arithmetic.
+__global__ __launch_bounds__(256) void quant_act1_kernel(QuantActArgs a)
 {
     const int nb = a.K >> 5;
     const int id = blockIdx.x * 8 + (threadIdx.x >> 5), i = threadIdx.x & 31;
@@ -59,9 +96,9 @@ __global__ __launch_bounds__(256) void quant_act_kernel(QuantActArgs a)
     a.xq[xq_index(t, 32 * b + i, nb)] = (int8_t)q;
     if (i == 0) {
         const size_t bi = (size_t)b * a.T16 + t;
-        a.xd[bi] = (float)(_Float16)d; // the stored Half scale
+        a.xd[bi] = (float)(_Float16)d;
         a.xqs[bi] = s;
-        a.xs[bi] = d * (float)s; // QuantMatMul's block sums use the float d
+        a.xs[bi] = d * (float)s;
     }
 }
 
@@ -69,8 +106,11 @@ hipError_t launch_quant_act(const QuantActArgs &a, hipStream_t s)
 {
     if (a.T <= 0) return hipSuccess;
     if (a.K <= 0 || a.K % 32 != 0 || a.T16 < ((a.T + 15) & ~15)) return hipErrorInvalidValue;
-    const long long halves = (long long)a.T * (a.K >> 5);
-    hipLaunchKernelGGL(quant_act_kernel, dim3((unsigned)((halves + 7) / 8)), dim3(256), 0, s, a);
+    const long long blocks = (long long)a.T * (a.K >> 5);
+    if (((uintptr_t)a.x & 15) == 0) // eight lanes per block, 32 blocks per workgroup
+        hipLaunchKernelGGL(quant_act_kernel, dim3((unsigned)((blocks + 31) / 32)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(quant_act1_kernel, dim3((unsigned)((blocks + 7) / 8)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -127,3 +127,28 @@ def test_gpu_resident_weight_integer_matches_hook_bitwise(integer, t, rows, cols
     w.close()
     want = matmul_gpu(t, raw, rows, cols, x, tokens)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gpu_integer_unaligned_input_gives_the_same_bits(integer, t):
+    # x one float past a 16-byte boundary takes the one-element activation
+    # quantizer instead of the four-element one: the same quants, scales and
+    # sums, so the same outputs
+    import torch
+    rows, cols, tokens = 384, 1088, 130
+    raw = reference_test_weights(t, rows, cols, 5)
+    x = np.random.default_rng(6).uniform(-1, 1, (tokens, cols)).astype(np.float32)
+    w = jev.QuantWeight(t, rows, cols, raw)
+    bx = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)])).to("cuda:0")
+    dx = torch.from_numpy(x).to("cuda:0")
+    dy0 = torch.empty((tokens, rows), dtype=torch.float32, device="cuda:0")
+    dy1 = torch.empty((tokens, rows), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    assert bx.data_ptr() % 16 == 0
+    w.matmul_device(bx.data_ptr() + 4, tokens, dy0.data_ptr())
+    w.matmul_device(dx.data_ptr(), tokens, dy1.data_ptr())
+    w.sync()
+    got, want = dy0.cpu().numpy(), dy1.cpu().numpy()
+    w.close()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(want.view(np.uint32), oracle.matmul_integer(t, raw, rows, cols, x, tokens).view(np.uint32))
