@@ -511,7 +511,29 @@ __global__ __launch_bounds__(256) void rows_step_kernel(const float *logits, int
     const float *x = logits + (size_t)r * vocab;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int k = threadIdx.x; k < vocab; k += 256) better(v, idx, x[k], k);
+    // eight 16-byte loads in flight per thread, then their elements in
+    // turn (one row per workgroup: a load-then-compare chain per element
+    // would wait on memory once per element); better() is a total order, so
+    // the order elements are taken in does not change the result
+    const int n4 = vocab % 4 == 0 && ((uintptr_t)x & 15) == 0 ? vocab / 4 : 0;
+    const float4 *x4 = (const float4 *)x;
+    constexpr int B = 8;
+    for (int base = 0; base < n4; base += 256 * B) {
+        float4 c[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) c[j] = x4[min(base + 256 * j + (int)threadIdx.x, n4 - 1)]; // clamped: unused copies
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const int e = base + 256 * j + threadIdx.x;
+            if (e < n4) {
+                better(v, idx, c[j].x, 4 * e);
+                better(v, idx, c[j].y, 4 * e + 1);
+                better(v, idx, c[j].z, 4 * e + 2);
+                better(v, idx, c[j].w, 4 * e + 3);
+            }
+        }
+    }
+    for (int k = 4 * n4 + threadIdx.x; k < vocab; k += 256) better(v, idx, x[k], k);
     bv[threadIdx.x] = v;
     bi[threadIdx.x] = idx;
     __syncthreads();
