@@ -51,19 +51,23 @@ __device__ __forceinline__ void split2_rtz(float x0, float x1, uint32_t &hi, uin
 // One weight element of the tiled layout, decoded exactly as Dequantizer
 // does (Dequantizer.cs: Q4_0 :155-182, Q5_1 :240-268, Q8_0 :270-305).  d*q is
 // exact in fp32, so the Q5_1 "+ m" rounds once whether or not it is fused.
+// TYPE >= 0: the weight's type known at compile time (no branches around the
+// loads, so a caller's loads of several elements can all be in flight).
+template <int TYPE = -1>
 __device__ __forceinline__ float decode_elem(const QWeight &w, int row, int k)
 {
+    const int type = TYPE >= 0 ? TYPE : w.type;
     const int rg = row >> 4, r = row & 15, b = k >> 5, kk = k & 31, g = kk >> 3, i = kk & 7, bb = b & 1;
     const int l = 16 * g + r;
     const size_t tile = (size_t)rg * tile_kpairs(w.cols) + (b >> 1);
-    const float d = h2f(w.type == kQ5_1 ? w.d[tile * 64 + 4 * r + bb] : w.d[tile * 32 + 2 * r + bb]);
-    if (w.type == kQ8_0) {
+    const float d = h2f(type == kQ5_1 ? w.d[tile * 64 + 4 * r + bb] : w.d[tile * 32 + 2 * r + bb]);
+    if (type == kQ8_0) {
         const int q = (int)w.qs[tile * 1024 + 16 * l + 8 * bb + i] - 128; // stored biased
         return (float)q * d;
     }
     const uint8_t byte = w.qs[tile * 512 + 8 * l + 4 * bb + (i & 3)];
     const int nib = i < 4 ? (byte & 15) : (byte >> 4);
-    if (w.type == kQ4_0) return d * (float)(nib - 8);
+    if (type == kQ4_0) return d * (float)(nib - 8);
     const int q = nib | (((w.qh[tile * 128 + 2 * l + bb] >> i) & 1) << 4);
     const float m = h2f(w.d[tile * 64 + 4 * r + 2 + bb]);
     const float dq = d * (float)q;

@@ -387,14 +387,29 @@ hipError_t launch_rope_store(const RopeArgs &a, hipStream_t s)
 
 // One wave per (output, selected row): the decoded row dotted with the
 // normalised output state (MinistralModel.cs:386-410), lane-strided fp32 FMA
-// chains reduced by a fixed butterfly.
+// chains reduced by a fixed butterfly.  Each lane's elements are taken eight
+// at a time, their loads (the state and the weight element's quant and scale)
+// all issued before the eight FMAs, which run in the chain's order.
+template <int TYPE>
 __global__ __launch_bounds__(64) void head_rows_kernel(HeadRowsArgs a)
 {
     int b = blockIdx.x, i = blockIdx.y;
     int r = a.rows[i];
     const float *x = a.xn + (size_t)b * a.D;
     float acc = 0.f;
-    for (int k = threadIdx.x; k < a.D; k += 64) acc = fmaf(x[k], decode_elem(a.table, r, k), acc);
+    constexpr int B = 8;
+    for (int k0 = threadIdx.x; k0 < a.D; k0 += 64 * B) {
+        float xv[B], wv[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const int k = min(k0 + 64 * j, a.D - 1); // clamped: unused copies
+            xv[j] = x[k];
+            wv[j] = decode_elem<TYPE>(a.table, r, k);
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++)
+            if (k0 + 64 * j < a.D) acc = fmaf(xv[j], wv[j], acc);
+    }
     acc = warp_sum(acc);
     if (threadIdx.x == 0) a.out[(size_t)b * a.n_rows + i] = acc;
 }
@@ -402,7 +417,13 @@ __global__ __launch_bounds__(64) void head_rows_kernel(HeadRowsArgs a)
 hipError_t launch_head_rows(const HeadRowsArgs &a, hipStream_t s)
 {
     if (a.n_out <= 0 || a.n_rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(head_rows_kernel, dim3(a.n_out, a.n_rows), dim3(64), 0, s, a);
+    const dim3 grid(a.n_out, a.n_rows);
+    switch (a.table.type) {
+    case kQ8_0: hipLaunchKernelGGL(head_rows_kernel<kQ8_0>, grid, dim3(64), 0, s, a); break;
+    case kQ4_0: hipLaunchKernelGGL(head_rows_kernel<kQ4_0>, grid, dim3(64), 0, s, a); break;
+    case kQ5_1: hipLaunchKernelGGL(head_rows_kernel<kQ5_1>, grid, dim3(64), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -435,7 +456,22 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float *x, const int32
     __shared__ int si[256];
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int k = blockIdx.x * 256 + threadIdx.x; k < n; k += gridDim.x * 256) better(v, idx, x[k], xi ? xi[k] : k);
+    // four candidates' loads in flight per thread, then their comparisons
+    // (better() is a total order: the order taken does not change the result)
+    const int stride = gridDim.x * 256;
+    for (int k0 = blockIdx.x * 256 + threadIdx.x; k0 < n; k0 += 4 * stride) {
+        float cv[4];
+        int ci[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int k = min(k0 + j * stride, n - 1); // clamped: unused copies
+            cv[j] = x[k];
+            ci[j] = xi ? xi[k] : k;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (k0 + j * stride < n) better(v, idx, cv[j], ci[j]);
+    }
     sv[threadIdx.x] = v;
     si[threadIdx.x] = idx;
     __syncthreads();
